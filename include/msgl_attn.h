@@ -1,0 +1,102 @@
+/*
+ * msgl_attn.h -- C ABI of the MI355X (gfx950) attention backend for
+ * mini-sglang-mlx's attention hot path.
+ *
+ * Every entry point takes plain device pointers and sizes (no framework
+ * types), enqueues work on the caller's HIP stream (`stream` is a hipStream_t,
+ * NULL = the null stream), never synchronises and never allocates: scratch
+ * memory is passed in by the caller. All functions return 0 on success or a
+ * MSGL_ERR_* code, with a message for the calling thread in msgl_last_error().
+ *
+ * Reference interfaces replaced (paths relative to the reference's
+ * python/minisgl_mlx/):
+ *   msgl_store_kv            kvcache/pool.py:47-50        MHAKVCache.store_kv
+ *   msgl_paged_decode        attention/metal.py:112-131   paged_decode_attention
+ *                            (semantics of attention/naive.py:50-60 forward_decode)
+ *   msgl_prefill_ragged      attention/base.py:85-105     BaseAttnBackend._forward_prefill
+ *   msgl_build_decode_meta   attention/metal.py:145-152   MetalAttnBackend.prepare_decode
+ *                            + scheduler/scheduler.py:154-157 (out_loc, positions)
+ *
+ * Layouts (identical to the reference, no transposes at the boundary):
+ *   q, out   [T, Hq, D]   row-major, dtype `dtype`
+ *   k, v     [T, Hkv, D]
+ *   pools    [num_slots, Hkv, D] one K and one V buffer per layer
+ *   indices  int32; q head h reads kv head h / (Hq / Hkv)
+ */
+#ifndef MSGL_ATTN_H_
+#define MSGL_ATTN_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MSGL_ABI_VERSION 1
+
+enum msgl_status {
+  MSGL_OK = 0,
+  MSGL_ERR_INVALID = 1,     /* bad argument (shape, null pointer, range)  */
+  MSGL_ERR_UNSUPPORTED = 2, /* valid but not built (dtype/head_dim/group) */
+  MSGL_ERR_WORKSPACE = 3,   /* workspace too small                        */
+  MSGL_ERR_HIP = 4          /* the HIP runtime reported an error          */
+};
+
+enum msgl_dtype { MSGL_F32 = 0, MSGL_BF16 = 1, MSGL_F16 = 2 };
+
+/* ABI version of the loaded library (MSGL_ABI_VERSION). */
+int msgl_abi_version(void);
+
+/* Message of the last failing call on this thread ("" if none). */
+const char* msgl_last_error(void);
+
+/*
+ * KV store: k_pool[out_loc[t]] = k[t]; v_pool[out_loc[t]] = v[t] for t < num_tokens.
+ * Replaces kvcache/pool.py:47-50 (called before attention, layers.py:109).
+ * Bit-exact row copy of Hkv*D elements. out_loc entries must be distinct
+ * (the allocator's invariant, scheduler/cache.py:124-132); an entry outside
+ * [0, num_slots) is skipped, never written.
+ */
+int msgl_store_kv(const void* k, const void* v, const int32_t* out_loc, void* k_pool, void* v_pool,
+                  int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
+                  int32_t dtype, void* stream);
+
+/* Default split count for msgl_paged_decode (max_splits <= 0 picks this). */
+int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len);
+
+/* Bytes of workspace msgl_paged_decode needs for these sizes. */
+int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
+                                         int32_t max_splits);
+
+/*
+ * Paged decode attention, one query token per request.
+ * Replaces attention/metal.py:112-131 (paged_decode_attention); the result
+ * equals attention/naive.py:50-60 (gather + masked SDPA) within fp tolerance.
+ *
+ *   q          [B, Hq, D]
+ *   kv_indptr  CSR offsets into kv_indices ([B+1]); when seq_lens != NULL only
+ *              kv_indptr[0..B-1] are read (start offsets, any order)
+ *   kv_indices page_size == 1: token slots (attention/metal.py:150);
+ *              page_size  > 1: page ids; token t of a request lives at slot
+ *              kv_indices[kv_indptr[b] + t / page_size] * page_size + t % page_size
+ *   seq_lens   [B] tokens per request, or NULL (then L_b = indptr[b+1]-indptr[b],
+ *              page_size must be 1)
+ *   scale      softmax scale (attention/base.py:45: head_dim ** -0.5)
+ *   max_splits split-K factor bound (<= 0: msgl_paged_decode_default_splits)
+ *   out        [B, Hq, D]
+ *   workspace  >= msgl_paged_decode_workspace_size(B, Hq, D, max_splits) bytes
+ * A request with L_b == 0 gets a zero output row. Slots outside
+ * [0, num_slots) are clamped to slot 0 (memory-safe; result unspecified).
+ */
+int msgl_paged_decode(const void* q, const void* k_pool, const void* v_pool, const int32_t* kv_indptr,
+                      const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                      int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                      int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MSGL_ATTN_H_ */

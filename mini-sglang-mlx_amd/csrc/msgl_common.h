@@ -1,0 +1,158 @@
+// Shared device helpers and host error channel for the gfx950 attention kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include <cstdio>
+#include <string>
+
+#include "msgl_attn.h"
+
+namespace msgl {
+
+// ---------------------------------------------------------------------------
+// host: per-thread error message and status helpers
+// ---------------------------------------------------------------------------
+void set_error(const char* fmt, ...);
+void clear_error();
+
+#define MSGL_CHECK_ARG(cond, ...)            \
+  do {                                       \
+    if (!(cond)) {                           \
+      ::msgl::set_error(__VA_ARGS__);        \
+      return MSGL_ERR_INVALID;               \
+    }                                        \
+  } while (0)
+
+#define MSGL_CHECK_LAUNCH(what)                                                          \
+  do {                                                                                   \
+    hipError_t err__ = hipGetLastError();                                                \
+    if (err__ != hipSuccess) {                                                           \
+      ::msgl::set_error("%s: HIP launch failed: %s", what, hipGetErrorString(err__));    \
+      return MSGL_ERR_HIP;                                                               \
+    }                                                                                    \
+  } while (0)
+
+inline int dtype_size(int32_t dtype) {
+  switch (dtype) {
+    case MSGL_F32: return 4;
+    case MSGL_BF16: return 2;
+    case MSGL_F16: return 2;
+    default: return 0;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// device: element types
+// ---------------------------------------------------------------------------
+typedef uint16_t bf16_t;  // raw bfloat16 bits
+typedef _Float16 f16_t;
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// float -> bfloat16, round to nearest even (NaN kept quiet).
+__device__ __forceinline__ uint16_t f32_to_bf16(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+// Unpack the 8 elements of a 16-byte chunk to fp32, for each storage type.
+template <typename T>
+struct Vec16;
+
+template <>
+struct Vec16<float> {
+  static constexpr int N = 4;
+  __device__ __forceinline__ static void to_f32(const u32x4& r, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) out[i] = __uint_as_float(r[i]);
+  }
+};
+
+template <>
+struct Vec16<bf16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void to_f32(const u32x4& r, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = __uint_as_float(r[i] << 16);
+      out[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
+    }
+  }
+};
+
+template <>
+struct Vec16<f16_t> {
+  static constexpr int N = 8;
+  __device__ __forceinline__ static void to_f32(const u32x4& r, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      out[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r[i] & 0xffffu));
+      out[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r[i] >> 16));
+    }
+  }
+};
+
+template <typename T>
+__device__ __forceinline__ T from_f32(float f);
+template <>
+__device__ __forceinline__ float from_f32<float>(float f) { return f; }
+template <>
+__device__ __forceinline__ bf16_t from_f32<bf16_t>(float f) { return f32_to_bf16(f); }
+template <>
+__device__ __forceinline__ f16_t from_f32<f16_t>(float f) { return (_Float16)f; }
+
+template <typename T>
+__device__ __forceinline__ float to_f32(T x);
+template <>
+__device__ __forceinline__ float to_f32<float>(float x) { return x; }
+template <>
+__device__ __forceinline__ float to_f32<bf16_t>(bf16_t x) { return bf16_to_f32(x); }
+template <>
+__device__ __forceinline__ float to_f32<f16_t>(f16_t x) { return (float)x; }
+
+// 16-byte global load / store (dwordx4).
+__device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
+
+// ---------------------------------------------------------------------------
+// device: cross-lane reductions inside one 16-lane DPP row
+// ---------------------------------------------------------------------------
+// DPP controls: quad_perm [1,0,3,2] = 0xB1, quad_perm [2,3,0,1] = 0x4E,
+// row_half_mirror = 0x141, row_mirror = 0x140. After the four steps every
+// lane of a 16-lane row holds the row's reduction.
+#define MSGL_DPP(v, ctrl) \
+  __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, (v)), (ctrl), 0xF, 0xF, true))
+
+__device__ __forceinline__ float row16_max(float v) {
+  v = fmaxf(v, MSGL_DPP(v, 0xB1));
+  v = fmaxf(v, MSGL_DPP(v, 0x4E));
+  v = fmaxf(v, MSGL_DPP(v, 0x141));
+  v = fmaxf(v, MSGL_DPP(v, 0x140));
+  return v;
+}
+
+__device__ __forceinline__ float row16_sum(float v) {
+  v += MSGL_DPP(v, 0xB1);
+  v += MSGL_DPP(v, 0x4E);
+  v += MSGL_DPP(v, 0x141);
+  v += MSGL_DPP(v, 0x140);
+  return v;
+}
+
+// Ordering point for LDS traffic between lanes of one wavefront.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
+}  // namespace msgl

@@ -1,0 +1,142 @@
+"""``hip`` attention backend: gfx950 kernels behind the reference's backend interface.
+
+Decode metadata is the CSR form of attention/metal.py:145-152
+(kv_indptr [B+1], kv_indices [sum L] token slots), built with numpy from the
+host page table and copied to the device once per step; every layer then
+runs one paged-decode launch (+ the split-K merge) over its own pool.
+Prefill metadata mirrors attention/base.py:70-83 and additionally carries the
+packed ragged description (q_indptr, kv_indptr, kv_indices, seq_lens) that
+the ragged prefill kernel reads in one launch instead of a per-request loop.
+
+Each step's index tensors are fresh device tensors, so a step that is still
+running on the stream never sees the next step's indices (the overlap loop of
+scheduler/scheduler.py:88-118 prepares step t+1 while step t runs).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import TYPE_CHECKING, Optional
+
+import numpy as np
+import torch
+
+from .. import ops
+from .base import BaseAttnBackend, PrefillMetadata
+
+if TYPE_CHECKING:
+    from minisgl_hip.core import Batch
+
+
+def _to_device(x: np.ndarray, device: torch.device) -> torch.Tensor:
+    t = torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32))
+    if device.type == "cuda":
+        return t.pin_memory().to(device, non_blocking=True)
+    return t.to(device)
+
+
+@dataclass
+class HipDecodeMetadata:
+    kv_indptr: torch.Tensor  # [B+1] int32, device
+    kv_indices: torch.Tensor  # [sum L] int32, device
+    max_seq_len: int
+    max_splits: int
+
+
+@dataclass
+class HipPrefillDevice:
+    q_indptr: torch.Tensor  # [R+1]
+    kv_indptr: torch.Tensor  # [R+1]
+    kv_indices: torch.Tensor  # [sum (P+E)] token slots
+    seq_lens: torch.Tensor  # [R]
+    max_extend_len: int
+    num_tokens: int
+
+
+class HipAttnBackend(BaseAttnBackend):
+    def __init__(self, config, kv_cache, page_table: np.ndarray) -> None:
+        super().__init__(config, kv_cache, page_table)
+        self.device = kv_cache.k_cache(0).device
+        self._workspace: Optional[torch.Tensor] = None
+
+    # ------------------------------------------------------------------ decode
+
+    def prepare_decode(self, batch: "Batch") -> HipDecodeMetadata:
+        """attention/metal.py:145-152 (CSR over token slots), then one H2D copy."""
+        lens = np.array([r.device_len for r in batch.reqs])
+        rows = np.array([r.table_idx for r in batch.reqs])
+        max_len = int(lens.max())
+        valid = np.arange(max_len)[None, :] < lens[:, None]
+        kv_indices = self.page_table[rows, :max_len][valid]
+        kv_indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+        splits = ops.default_splits(len(lens), self.config.num_kv_heads, max_len)
+        return HipDecodeMetadata(
+            kv_indptr=_to_device(kv_indptr, self.device),
+            kv_indices=_to_device(kv_indices, self.device),
+            max_seq_len=max_len,
+            max_splits=splits,
+        )
+
+    def _decode_workspace(self, batch_size: int, max_splits: int) -> Optional[torch.Tensor]:
+        need = ops.decode_workspace_bytes(batch_size, self.config.num_qo_heads, self.config.head_dim, max_splits)
+        if need == 0:
+            return None
+        if self._workspace is None or self._workspace.numel() < need:
+            # one buffer reused by every layer: layers run in stream order
+            self._workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
+        return self._workspace
+
+    def forward_decode(self, q: torch.Tensor, layer_id: int, meta: HipDecodeMetadata) -> torch.Tensor:
+        ws = self._decode_workspace(q.shape[0], meta.max_splits)
+        return ops.paged_decode_attention(
+            q,
+            self.kv_cache.k_cache(layer_id),
+            self.kv_cache.v_cache(layer_id),
+            meta.kv_indptr,
+            meta.kv_indices,
+            self.scale,
+            max_splits=meta.max_splits,
+            workspace=ws,
+        )
+
+    # ------------------------------------------------------------------ prefill
+
+    def _prepare_prefill(self, batch: "Batch") -> PrefillMetadata:
+        """attention/base.py:70-83, plus the packed ragged form for one kernel launch."""
+        extend_lens = [r.extend_len for r in batch.reqs]
+        q_offsets = np.concatenate([[0], np.cumsum(extend_lens)]).tolist()
+        kv_indices = []
+        flat = []
+        for req in batch.reqs:
+            row = self.page_table[req.table_idx, : req.device_len]
+            kv_indices.append(None if req.cached_len == 0 else row.copy())
+            flat.append(row)
+        seq_lens = np.array([r.device_len for r in batch.reqs], dtype=np.int32)
+        dev = HipPrefillDevice(
+            q_indptr=_to_device(np.asarray(q_offsets, dtype=np.int32), self.device),
+            kv_indptr=_to_device(np.concatenate([[0], np.cumsum(seq_lens)]).astype(np.int32), self.device),
+            kv_indices=_to_device(np.concatenate(flat), self.device),
+            seq_lens=_to_device(seq_lens, self.device),
+            max_extend_len=int(max(extend_lens)),
+            num_tokens=int(q_offsets[-1]),
+        )
+        return PrefillMetadata(
+            last_indices=_to_device(np.array(q_offsets[1:], dtype=np.int32) - 1, self.device),
+            q_offsets=q_offsets,
+            kv_indices=kv_indices,
+            device=dev,
+        )
+
+    def _forward_prefill(self, q, k, v, layer_id: int, meta: PrefillMetadata) -> torch.Tensor:
+        d = meta.device
+        return ops.prefill_ragged_attention(
+            q,
+            self.kv_cache.k_cache(layer_id),
+            self.kv_cache.v_cache(layer_id),
+            d.q_indptr,
+            d.kv_indptr,
+            d.kv_indices,
+            d.seq_lens,
+            self.scale,
+            max_extend_len=d.max_extend_len,
+        )

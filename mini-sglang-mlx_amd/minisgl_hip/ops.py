@@ -1,0 +1,127 @@
+"""torch-facing wrappers of the HIP kernels (argument checks + one C-ABI call each).
+
+Tensors stay on the caller's device; work is enqueued on the current stream
+and nothing synchronises. Preconditions raise ``ValueError`` like the
+reference's asserts (attention/metal.py:122); kernel/runtime failures raise
+``RuntimeError`` with the library's message.
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Union
+
+import torch
+
+from . import _lib
+
+
+def _check_device(name: str, t: torch.Tensor, device: torch.device) -> None:
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _check_index(name: str, t: Optional[torch.Tensor], device: torch.device) -> None:
+    if t is None:
+        return
+    if t.dtype != torch.int32:
+        raise ValueError(f"{name} must be int32 (got {t.dtype})")
+    _check_device(name, t, device)
+
+
+def store_kv(
+    k: torch.Tensor, v: torch.Tensor, out_loc: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor
+) -> None:
+    """k_pool[out_loc] = k; v_pool[out_loc] = v (kvcache/pool.py:47-50), in place."""
+    if k.dim() != 3 or k.shape != v.shape:
+        raise ValueError(f"k/v must both be [T, Hkv, D] (got {tuple(k.shape)}, {tuple(v.shape)})")
+    if k_pool.dim() != 3 or k_pool.shape != v_pool.shape or k_pool.shape[1:] != k.shape[1:]:
+        raise ValueError(f"pools must be [N, Hkv, D] matching k (got {tuple(k_pool.shape)})")
+    if out_loc.dim() != 1 or out_loc.shape[0] != k.shape[0]:
+        raise ValueError("out_loc must be [T]")
+    if len({k.dtype, v.dtype, k_pool.dtype, v_pool.dtype}) != 1:
+        raise ValueError("k, v and pools must share one dtype")
+    dev = k_pool.device
+    for name, t in (("k", k), ("v", v), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _check_device(name, t, dev)
+    _check_index("out_loc", out_loc, dev)
+    lib = _lib.load()
+    status = lib.msgl_store_kv(
+        _lib.ptr(k), _lib.ptr(v), _lib.ptr(out_loc), _lib.ptr(k_pool), _lib.ptr(v_pool),
+        k.shape[0], k.shape[1], k.shape[2], k_pool.shape[0], _lib.dtype_code(k.dtype),
+        _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_store_kv")
+
+
+def default_splits(batch: int, num_kv_heads: int, max_seq_len: int = 0) -> int:
+    return int(_lib.load().msgl_paged_decode_default_splits(batch, num_kv_heads, max_seq_len))
+
+
+def decode_workspace_bytes(batch: int, num_qo_heads: int, head_dim: int, max_splits: int) -> int:
+    return int(_lib.load().msgl_paged_decode_workspace_size(batch, num_qo_heads, head_dim, max_splits))
+
+
+def paged_decode_attention(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    kv_indices: torch.Tensor,
+    scale: Union[float, torch.Tensor],
+    *,
+    seq_lens: Optional[torch.Tensor] = None,
+    page_size: int = 1,
+    max_splits: Optional[int] = None,
+    max_seq_len: int = 0,
+    out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Paged decode attention; counterpart of attention/metal.py:112-131.
+
+    q [B, Hq, D]; pools [N, Hkv, D]; kv_indptr [B+1] int32; kv_indices int32
+    (token slots, or page ids when page_size > 1 with seq_lens [B] given).
+    Returns o [B, Hq, D] in q's dtype.
+    """
+    if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
+        raise ValueError("q must be [B, Hq, D] and pools [N, Hkv, D]")
+    b, hq, d = q.shape
+    n_slots, hkv, dk = k_pool.shape
+    if dk != d or hq % hkv != 0:
+        raise ValueError(f"head_dim mismatch or Hq ({hq}) not a multiple of Hkv ({hkv})")
+    if len({q.dtype, k_pool.dtype, v_pool.dtype}) != 1:
+        raise ValueError("q and pools must share one dtype")
+    if page_size > 1 and seq_lens is None:
+        raise ValueError("page_size > 1 needs seq_lens")
+    if kv_indptr.dim() != 1 or kv_indptr.shape[0] < b + (0 if seq_lens is not None else 1):
+        raise ValueError("kv_indptr must be [B+1]")
+    dev = q.device
+    for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _check_device(name, t, dev)
+    for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices), ("seq_lens", seq_lens)):
+        _check_index(name, t, dev)
+    if isinstance(scale, torch.Tensor):
+        scale = float(scale.reshape(-1)[0].item())
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _check_device("out", out, dev)
+        if out.shape != q.shape or out.dtype != q.dtype:
+            raise ValueError("out must match q's shape and dtype")
+    lib = _lib.load()
+    if max_splits is None:
+        max_splits = int(lib.msgl_paged_decode_default_splits(b, hkv, max_seq_len))
+    need = int(lib.msgl_paged_decode_workspace_size(b, hq, d, max_splits))
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    status = lib.msgl_paged_decode(
+        _lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool),
+        _lib.ptr(kv_indptr), _lib.ptr(kv_indices), _lib.ptr(seq_lens),
+        b, hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
+        max_splits, _lib.ptr(out), _lib.ptr(workspace),
+        0 if workspace is None else workspace.numel() * workspace.element_size(),
+        _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_paged_decode")
+    return out

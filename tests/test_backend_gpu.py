@@ -1,0 +1,68 @@
+"""The backend behind the reference's interface, driven in the caller's order
+(layers.py:107-110: store_kv, then attn_backend.forward), over several layers
+and decode steps, checked against the oracle."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import assert_close, i32, randn, to_np64
+from minisgl_hip.attention import create_attention_backend
+from minisgl_hip.core import Batch, ModelConfig, Req
+from minisgl_hip.kvcache import MHAKVCache
+
+pytestmark = pytest.mark.gpu
+
+
+def _setup(device, dtype, num_layers=3, num_tokens=8192, max_req=8, max_len=1024, page_size=1):
+    cfg = ModelConfig(num_qo_heads=16, num_kv_heads=8, head_dim=128, num_layers=num_layers)
+    kv = MHAKVCache(num_layers, num_tokens, 8, 128, dtype, device)
+    table = np.zeros((max_req, max_len), dtype=np.int32)
+    backend = create_attention_backend("hip", cfg, kv, table)
+    return cfg, kv, table, backend
+
+
+def test_decode_steps_through_backend(cuda_device):
+    dt = torch.bfloat16
+    cfg, kv, table, backend = _setup(cuda_device, dt)
+    rng = np.random.default_rng(0)
+    free = rng.permutation(8192).astype(np.int32)
+    # three requests with cached histories (prefill already done): fill pools with history
+    reqs = []
+    for i, n in enumerate([40, 300, 7]):
+        reqs.append(Req(input_ids=np.zeros(n + 1, np.int32), table_idx=i + 2, cached_len=n))
+    free = oracle.allocate_paged(table, free, [r.table_idx for r in reqs], [0] * 3, [r.cached_len for r in reqs], 1)
+    for layer in range(cfg.num_layers):
+        kv.k[layer].copy_(randn(kv.k[layer].shape, 10 + layer, dt).to(cuda_device))
+        kv.v[layer].copy_(randn(kv.v[layer].shape, 20 + layer, dt).to(cuda_device))
+    for step in range(2):
+        batch = Batch(reqs=reqs, phase="decode")
+        free = oracle.allocate_paged(table, free, [r.table_idx for r in reqs], [r.cached_len for r in reqs],
+                                     [r.device_len for r in reqs], 1)
+        pos, out_loc = oracle.prepare_batch_indices(table, [r.table_idx for r in reqs],
+                                                    [r.cached_len for r in reqs], [r.device_len for r in reqs])
+        batch.positions = i32(pos, cuda_device)
+        batch.out_loc = i32(out_loc, cuda_device)
+        backend.prepare_metadata(batch)
+        # the device metadata is the CSR form of attention/metal.py:145-152, bit-exact
+        lens = [r.device_len for r in reqs]
+        indptr, indices = oracle.csr_decode_metadata(table, [r.table_idx for r in reqs], lens)
+        assert np.array_equal(batch.attn_metadata.kv_indptr.cpu().numpy(), indptr)
+        assert np.array_equal(batch.attn_metadata.kv_indices.cpu().numpy(), indices)
+        for layer in range(cfg.num_layers):
+            q = randn((3, 16, 128), 100 * step + layer, dt).to(cuda_device)
+            k = randn((3, 8, 128), 200 * step + layer, dt).to(cuda_device)
+            v = randn((3, 8, 128), 300 * step + layer, dt).to(cuda_device)
+            print(f"case backend step={step} layer={layer}", flush=True)
+            kv.store_kv(k, v, batch.out_loc, layer)
+            o = backend.forward(q, k, v, layer, batch)
+            torch.cuda.synchronize()
+            kvi, mask = oracle.naive_decode_metadata(table, [r.table_idx for r in reqs], lens)
+            ref = oracle.naive_forward_decode(to_np64(q), to_np64(kv.k[layer]), to_np64(kv.v[layer]), kvi, mask,
+                                              cfg.head_dim**-0.5)
+            assert_close(o, ref, dt, f"backend step {step} layer {layer}")
+            # the new token's row landed at out_loc
+            assert torch.equal(kv.k[layer][batch.out_loc.long()], k)
+        for r in reqs:
+            r.complete_one()

@@ -1,0 +1,85 @@
+"""C ABI checks that need no GPU: the library loads, exports every function
+declared in include/*.h with the signature the binding declares, and rejects
+bad arguments on the host before any device work."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from minisgl_hip import _lib
+
+INCLUDE = Path(__file__).resolve().parent.parent / "include"
+
+
+def declared_functions():
+    names = set()
+    for h in INCLUDE.glob("*.h"):
+        text = h.read_text()
+        text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+        for m in re.finditer(r"\b(msgl_\w+)\s*\(", text):
+            names.add(m.group(1))
+    return names
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    names = declared_functions()
+    assert names, "no declarations found"
+    for name in sorted(names):
+        assert hasattr(lib, name), f"{name} declared in include/ but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature"
+    assert set(_lib.SIGNATURES) == names
+
+
+def test_abi_version_and_sizes():
+    lib = _lib.load()
+    assert lib.msgl_abi_version() == 1
+    assert lib.msgl_paged_decode_workspace_size(128, 16, 128, 1) == 0
+    ws = lib.msgl_paged_decode_workspace_size(128, 16, 128, 16)
+    units = 128 * 16 * 16
+    assert ws == ((units * 128 * 4 + 255) // 256) * 256 + units * 8
+    assert 1 <= lib.msgl_paged_decode_default_splits(128, 8, 2048) <= 64
+    assert lib.msgl_paged_decode_default_splits(1, 8, 32768) == 64
+    assert lib.msgl_paged_decode_default_splits(1, 8, 100) == 2  # capped by ceil(100 / 64)
+
+
+def test_host_side_argument_errors():
+    lib = _lib.load()
+    nul = None
+    # Hq not a multiple of Hkv
+    st = lib.msgl_paged_decode(1, 1, 1, 1, 1, nul, 1, 6, 4, 128, 1, 100, _lib.MSGL_BF16, 0.1, 1, 1, nul, 0, nul)
+    assert st == _lib.MSGL_ERR_INVALID and "multiple" in _lib.last_error()
+    # unknown dtype
+    st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 1, 16, 8, 128, 1, 100, 9, 0.1, 1, 16, nul, 0, nul)
+    assert st == _lib.MSGL_ERR_UNSUPPORTED
+    # page_size > 1 without seq_lens
+    st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 1, 16, 8, 128, 16, 100, 1, 0.1, 1, 16, nul, 0, nul)
+    assert st == _lib.MSGL_ERR_INVALID and "seq_lens" in _lib.last_error()
+    # workspace too small for split-K
+    st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 4, 16, 8, 128, 1, 100, 1, 0.1, 8, 16, nul, 0, nul)
+    assert st == _lib.MSGL_ERR_WORKSPACE
+    # unsupported head_dim is reported (dispatch happens before any launch)
+    st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 1, 16, 8, 96, 1, 100, 1, 0.1, 1, 16, nul, 0, nul)
+    assert st == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
+    # store_kv: zero tokens is a no-op; bad row size is unsupported
+    assert lib.msgl_store_kv(nul, nul, nul, nul, nul, 0, 8, 128, 10, 1, nul) == _lib.MSGL_OK
+    assert lib.msgl_store_kv(16, 16, 16, 16, 16, 4, 1, 3, 10, 1, nul) == _lib.MSGL_ERR_UNSUPPORTED
+    assert lib.msgl_store_kv(16, 16, 16, 16, 16, 4, 8, 128, 10, 7, nul) == _lib.MSGL_ERR_UNSUPPORTED
+    assert lib.msgl_store_kv(16, 16, 16, 16, 16, -1, 8, 128, 10, 1, nul) == _lib.MSGL_ERR_INVALID
+
+
+def test_python_wrapper_raises():
+    import torch
+
+    from minisgl_hip import ops
+
+    q = torch.zeros(2, 6, 64)
+    pool = torch.zeros(8, 4, 64)
+    with pytest.raises(ValueError):
+        ops.paged_decode_attention(q, pool, pool, torch.zeros(3, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), 0.1)
+    with pytest.raises(ValueError):
+        ops.store_kv(torch.zeros(2, 4, 64), torch.zeros(2, 4, 64), torch.zeros(3, dtype=torch.int32), pool, pool)
+    with pytest.raises(ValueError):
+        _lib.dtype_code(torch.int8)

@@ -1,0 +1,192 @@
+"""Paged decode on the GPU vs the float64 oracle (attention/naive.py:50-60 semantics).
+
+Shape grid and edge lengths follow tests/test_attention.py:19-39; the larger
+cases are BASELINE's decode workloads (checked on sampled requests, plus
+size-independent properties at full size).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import DTYPES, assert_close, i32, randn, to_np64
+from minisgl_hip import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _pools(n, hkv, d, dtype, seed, device):
+    k = randn((n, hkv, d), seed, dtype).to(device)
+    v = randn((n, hkv, d), seed + 1, dtype).to(device)
+    return k, v
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256)])
+@pytest.mark.parametrize("splits", [1, None, 8])
+def test_reference_grid(cuda_device, hq, hkv, d, dtype, splits):
+    """tests/test_attention.py:19-39: N=4096, B=7, lens [1,2,17,31,32,33,700], rng(0) permuted slots."""
+    dt = DTYPES[dtype]
+    c = workloads.reference_test_case()
+    kp, vp = _pools(4096, hkv, d, dt, 100, cuda_device)
+    q = randn((7, hq, d), 102, dt).to(cuda_device)
+    print(f"case grid hq={hq} hkv={hkv} d={d} {dtype} splits={splits}", flush=True)
+    out = ops.paged_decode_attention(
+        q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device), d**-0.5, max_splits=splits
+    )
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(to_np64(q), to_np64(kp), to_np64(vp), c.kv_indptr, c.kv_indices, d**-0.5)
+    assert_close(out, ref, dt, f"grid {hq}/{hkv}/{d} {dtype} splits={splits}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("splits", [1, 4, 64])
+def test_edge_lengths(cuda_device, dtype, splits):
+    """Lengths around the 16-token tile, the 64-token index block and split boundaries."""
+    dt = DTYPES[dtype]
+    lens = [1, 15, 16, 17, 63, 64, 65, 127, 128, 129, 1000, 4097]
+    c = workloads.decode_case_from_lens(lens, num_slots=8192, seed=7)
+    kp, vp = _pools(8192, 8, 128, dt, 200, cuda_device)
+    q = randn((len(lens), 16, 128), 202, dt).to(cuda_device)
+    print(f"case edge {dtype} splits={splits}", flush=True)
+    out = ops.paged_decode_attention(
+        q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device), 128**-0.5, max_splits=splits
+    )
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(to_np64(q), to_np64(kp), to_np64(vp), c.kv_indptr, c.kv_indices, 128**-0.5)
+    assert_close(out, ref, dt, f"edge {dtype} splits={splits}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_page_size_16_page_ids(cuda_device, dtype):
+    """page ids + seq_lens (page_size 16) equal the token-slot CSR form."""
+    dt = DTYPES[dtype]
+    lens = [1, 15, 16, 17, 200, 1023, 3000]
+    c = workloads.decode_case_from_lens(lens, num_slots=16384, page_size=16, seed=11)
+    kp, vp = _pools(16384, 8, 128, dt, 300, cuda_device)
+    q = randn((len(lens), 32, 128), 302, dt).to(cuda_device)
+    print(f"case page16 {dtype}", flush=True)
+    out = ops.paged_decode_attention(
+        q, kp, vp, i32(c.page_indptr, cuda_device), i32(c.page_ids, cuda_device), 128**-0.5,
+        seq_lens=i32(c.lens, cuda_device), page_size=16,
+    )
+    out_tok = ops.paged_decode_attention(
+        q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device), 128**-0.5
+    )
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(
+        to_np64(q), to_np64(kp), to_np64(vp), c.page_indptr, c.page_ids, 128**-0.5, page_size=16, seq_lens=c.lens
+    )
+    assert_close(out, ref, dt, f"page16 {dtype}")
+    assert torch.equal(out, out_tok), "page-id and token-slot forms differ"
+
+
+def test_table_rows_with_seq_lens(cuda_device):
+    """kv_indptr as row starts into a flattened token-granular page table (+ seq_lens)."""
+    dt = torch.bfloat16
+    c = workloads.decode_case_from_lens([5, 300, 77, 1], num_slots=4096, seed=12)
+    stride = c.page_table.shape[1]
+    starts = (np.arange(4) * stride).astype(np.int32)
+    kp, vp = _pools(4096, 8, 128, dt, 400, cuda_device)
+    q = randn((4, 16, 128), 402, dt).to(cuda_device)
+    print("case table-rows", flush=True)
+    out = ops.paged_decode_attention(
+        q, kp, vp, i32(starts, cuda_device), i32(c.page_table.reshape(-1), cuda_device), 128**-0.5,
+        seq_lens=i32(c.lens, cuda_device),
+    )
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(to_np64(q), to_np64(kp), to_np64(vp), c.kv_indptr, c.kv_indices, 128**-0.5)
+    assert_close(out, ref, dt, "table rows")
+
+
+def test_zero_length_request_gives_zeros(cuda_device):
+    dt = torch.bfloat16
+    lens = np.array([3, 0, 70], dtype=np.int32)
+    indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    indices = np.arange(73, dtype=np.int32)
+    kp, vp = _pools(128, 8, 128, dt, 500, cuda_device)
+    q = randn((3, 16, 128), 502, dt).to(cuda_device)
+    print("case zero-length", flush=True)
+    for splits in (1, 8):
+        out = ops.paged_decode_attention(q, kp, vp, i32(indptr, cuda_device), i32(indices, cuda_device), 0.1,
+                                         max_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.count_nonzero(out[1]) == 0
+        ref = oracle.paged_decode(to_np64(q[[0, 2]]), to_np64(kp), to_np64(vp),
+                                  np.array([0, 3, 73]), indices, 0.1)
+        assert_close(out[[0, 2]], ref, dt, "zero-length neighbours")
+
+
+def test_cfg1_fp32_full(cuda_device):
+    """B=8, L ~ U[100,1024], pool 16384, page 1, fp32: every request vs the oracle at 1e-5."""
+    c = workloads.decode_case(8, 100, 1024, 16384, 1, seed=0)
+    dt = torch.float32
+    kp, vp = _pools(16384, 8, 128, dt, 600, cuda_device)
+    q = randn((8, 16, 128), 602, dt).to(cuda_device)
+    print("case cfg1", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device),
+                                     128**-0.5)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(to_np64(q), to_np64(kp), to_np64(vp), c.kv_indptr, c.kv_indices, 128**-0.5)
+    assert_close(out, ref, dt, "cfg1")
+
+
+def _sampled_ref(q, kp, vp, c, pick, scale, page_size=1):
+    """Oracle on a subset of requests (gathering only their slots)."""
+    outs = []
+    for b in pick:
+        if page_size == 1:
+            slots = c.kv_indices[c.kv_indptr[b] : c.kv_indptr[b + 1]].astype(np.int64)
+        else:
+            slots = oracle.expand_page_indices(c.page_ids[c.page_indptr[b] : c.page_indptr[b + 1]], page_size,
+                                               int(c.lens[b]))
+        st = torch.from_numpy(slots).to(kp.device)
+        kb = to_np64(kp.index_select(0, st))
+        vb = to_np64(vp.index_select(0, st))
+        outs.append(oracle.sdpa(to_np64(q[b])[:, None, :], kb.transpose(1, 0, 2), vb.transpose(1, 0, 2), scale)[:, 0])
+    return np.stack(outs)
+
+
+def test_cfg2_full_size(cuda_device):
+    """Batch 128, L ~ U[200,2048], pool 262144, bf16: sampled requests vs oracle, plus
+    bitwise invariance under relocation of the KV rows and run-to-run determinism."""
+    c = workloads.decode_case(128, 200, 2048, 262144, 1, seed=0)
+    dt = torch.bfloat16
+    kp, vp = _pools(262144, 8, 128, dt, 700, cuda_device)
+    q = randn((128, 16, 128), 702, dt).to(cuda_device)
+    indptr, indices = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    print("case cfg2", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, indptr, indices, 128**-0.5)
+    out2 = ops.paged_decode_attention(q, kp, vp, indptr, indices, 128**-0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "decode is not deterministic"
+    pick = [0, 1, 17, 63, 64, 100, 126, 127]
+    ref = _sampled_ref(q, kp, vp, c, pick, 128**-0.5)
+    assert_close(out[pick], ref, dt, "cfg2 sampled")
+    # relocate every used row to a new slot (a fixed permutation of the pool): same bits out
+    perm = torch.from_numpy(np.random.default_rng(5).permutation(262144).astype(np.int64)).to(cuda_device)
+    kp2 = torch.empty_like(kp)
+    vp2 = torch.empty_like(vp)
+    kp2[perm] = kp
+    vp2[perm] = vp
+    out3 = ops.paged_decode_attention(q, kp2, vp2, indptr, perm[indices.long()].int(), 128**-0.5)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out3), "result depends on where the rows live"
+
+
+def test_cfg3_long_contexts_page16(cuda_device):
+    """Qwen3-8B heads (32/8/128), page 16, contexts 1024..8192 (reduced batch), split-K + merge."""
+    c = workloads.decode_case(24, 1024, 8192, 1 << 20, 16, seed=0)
+    dt = torch.bfloat16
+    kp, vp = _pools(1 << 20, 8, 128, dt, 800, cuda_device)
+    q = randn((24, 32, 128), 802, dt).to(cuda_device)
+    print("case cfg3-reduced", flush=True)
+    out = ops.paged_decode_attention(
+        q, kp, vp, i32(c.page_indptr, cuda_device), i32(c.page_ids, cuda_device), 128**-0.5,
+        seq_lens=i32(c.lens, cuda_device), page_size=16,
+    )
+    torch.cuda.synchronize()
+    pick = list(range(0, 24, 3))
+    ref = _sampled_ref(q, kp, vp, c, pick, 128**-0.5, page_size=16)
+    assert_close(out[pick], ref, dt, "cfg3 sampled")
