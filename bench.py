@@ -1,0 +1,228 @@
+"""Benchmark: paged decode attention on one MI355X (the attention hot path).
+
+One step = one decode step of Qwen3-0.6B attention over all 28 layers for a
+batch of 128 requests with ragged contexts U[200, 2048] (seed 0), page size 1,
+a 262144-slot bf16 KV pool per layer with randomly permuted slots: per layer,
+the new token's K/V rows are scattered into their slots (KV store) and paged
+decode attention runs over the pool. Inputs are resident in HBM before timing.
+
+Prints one JSON line. ``value`` is algorithmic GB/s over the whole step
+(decode bytes = ΣL·Hkv·D·2·2 + B·Hq·D·2·2 + ΣL·4 + (B+1)·4 per layer, plus the
+KV store's read+write); ``roofline`` is the decode launch alone (HIP events
+around every decode call inside the timed region, on the launch stream);
+``cpu_baseline`` times the CPU restatement of the reference's naive backend.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "mini-sglang-mlx_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import numpy as np  # noqa: E402
+
+HBM_PEAK_GBS = 8000.0
+METRIC = "paged-decode HBM GB/s (% of peak) + µs/layer at batch 128, Qwen3-0.6B shapes"
+HQ, HKV, D, LAYERS = 16, 8, 128, 28
+BATCH, LO, HI, POOL = 128, 200, 2048, 262144
+TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_cfg2_traffic.txt"
+
+
+def parse_args():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def read_traffic():
+    """HBM bytes per decode launch measured with rocprofv3 counters (see the file), or None."""
+    if not TRAFFIC_FILE.exists():
+        return None
+    for line in TRAFFIC_FILE.read_text().splitlines():
+        if line.startswith("traffic_bytes_per_launch:"):
+            return float(line.split(":", 1)[1].strip())
+    return None
+
+
+def cpu_baseline(seconds: float):
+    """The oracle's naive decode (attention/naive.py:36-60 restated in numpy, fp32)
+    on the CPU reference config (B=8, L ~ U[100,1024], pool 16384, fp32) and on
+    a 16-request sample of the benchmark batch; best of repeated runs."""
+    import threadpoolctl
+
+    import oracle
+    from minisgl_hip import workloads
+
+    cores = len(os.sched_getaffinity(0))
+    cores = min(cores, 16)
+    results = {}
+    with threadpoolctl.threadpool_limits(cores):
+        info = threadpoolctl.threadpool_info()
+        threads = max([i.get("num_threads", 1) for i in info] or [1])
+        cases = {
+            "cfg1": (workloads.decode_case(8, 100, 1024, 16384, 1, seed=0), 16384),
+            "cfg2_sample16": (workloads.decode_case(BATCH, LO, HI, POOL, 1, seed=0), POOL),
+        }
+        for name, (c, n) in cases.items():
+            rng = np.random.default_rng(1)
+            b = 8 if name == "cfg1" else 16
+            lens = c.lens[:b]
+            # random values tiled over the pool (the timing does not depend on them)
+            block = rng.standard_normal(1 << 22, dtype=np.float32)
+            kp = np.resize(block, (n, HKV, D))
+            vp = np.resize(block[::-1], (n, HKV, D))
+            q = rng.standard_normal((b, HQ, D), dtype=np.float32)
+            kvi, mask = oracle.naive_decode_metadata(c.page_table[:b], np.arange(b), lens)
+            nbytes = workloads.decode_bytes(lens, HQ, HKV, D, 4)
+            times = []
+            t_end = time.perf_counter() + seconds / 2
+            while time.perf_counter() < t_end or len(times) < 3:
+                t0 = time.perf_counter()
+                oracle.naive_forward_decode(q, kp, vp, kvi, mask, D**-0.5, acc_dtype=np.float32)
+                times.append(time.perf_counter() - t0)
+            best = min(times)
+            results[name] = {
+                "us_per_layer": best * 1e6,
+                "gbs": nbytes / best / 1e9,
+                "runs": len(times),
+                "batch": b,
+                "sum_len": int(lens.sum()),
+            }
+    return results, threads
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the attention path has no cross-GPU work in this build "
+              "(multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    from minisgl_hip import ops, workloads
+
+    dev = torch.device("cuda:0")
+    c = workloads.decode_case(BATCH, LO, HI, POOL, 1, seed=0)
+    dec_bytes = workloads.decode_bytes(c.lens, HQ, HKV, D, 2)
+    store_bytes = BATCH * HKV * D * 2 * 2 * 2  # K and V rows, read + written
+    step_bytes = LAYERS * (dec_bytes + store_bytes)
+
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(0)
+    kps = [torch.randn((POOL, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    vps = [torch.randn((POOL, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    qs = [torch.randn((BATCH, HQ, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    ks = [torch.randn((BATCH, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    vs = [torch.randn((BATCH, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    outs = [torch.empty_like(q) for q in qs]
+    indptr = torch.from_numpy(c.kv_indptr).to(dev)
+    indices = torch.from_numpy(c.kv_indices).to(dev)
+    out_loc = torch.from_numpy(c.out_loc).to(dev)
+    splits = args.splits or ops.default_splits(BATCH, HKV, int(c.lens.max()))
+    ws = torch.empty(max(1, ops.decode_workspace_bytes(BATCH, HQ, D, splits)), dtype=torch.uint8, device=dev)
+    scale = D**-0.5
+
+    def step(events=None):
+        for layer in range(LAYERS):
+            ops.store_kv(ks[layer], vs[layer], out_loc, kps[layer], vps[layer])
+            if events is not None:
+                events[layer][0].record()
+            ops.paged_decode_attention(qs[layer], kps[layer], vps[layer], indptr, indices, scale,
+                                       max_splits=splits, out=outs[layer], workspace=ws)
+            if events is not None:
+                events[layer][1].record()
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+
+    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in range(LAYERS)]
+          for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for s in range(args.steps):
+        step(ev[s])
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+
+    dec_ms = [e0.elapsed_time(e1) for st in ev for (e0, e1) in st]
+    dec_avg_s = float(np.mean(dec_ms)) / 1e3
+    ms_per_step = elapsed / args.steps * 1e3
+    value = step_bytes / (elapsed / args.steps) / 1e9
+    achieved = dec_bytes / dec_avg_s / 1e9
+    traffic = read_traffic()
+
+    cpu = None
+    if not args.no_cpu:
+        res, threads = cpu_baseline(args.cpu_seconds)
+        cpu = {
+            "value": round(res["cfg1"]["gbs"], 3),
+            "unit": "GB/s",
+            "cores": threads,
+            "kind": "port",
+            "sample": (
+                "numpy fp32 restatement of the naive backend (attention/naive.py:36-60: padded gather, mask, "
+                f"softmax attention), best of {res['cfg1']['runs']} runs on the CPU reference config "
+                f"(B=8, L~U[100,1024] seed 0, ΣL={res['cfg1']['sum_len']}, pool 16384, 16q/8kv/128); "
+                f"{res['cfg1']['us_per_layer']:.0f} µs/layer. Same code on the first 16 requests of the "
+                f"benchmark batch (bf16 values as fp32, ΣL={res['cfg2_sample16']['sum_len']}): "
+                f"{res['cfg2_sample16']['us_per_layer']:.0f} µs/layer = {res['cfg2_sample16']['gbs']:.2f} GB/s"
+            ),
+            "us_per_layer": round(res["cfg1"]["us_per_layer"], 1),
+            "cfg2_sample16_gbs": round(res["cfg2_sample16"]["gbs"], 3),
+        }
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": (
+                "paged decode, Qwen3-0.6B attention (16 q / 8 kv heads, head_dim 128), 28 layers; batch 128, "
+                "context U[200,2048] (seed 0), page_size 1, 262144-slot bf16 pool per layer, random slots; "
+                "per layer: KV-store scatter of the new token + paged decode"
+            ),
+            "batch": BATCH,
+            "sum_context": int(c.lens.sum()),
+            "layers": LAYERS,
+            "max_splits": splits,
+        },
+        "us_per_layer": round(ms_per_step * 1e3 / LAYERS, 2),
+        "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+        "decode_us_per_layer": round(dec_avg_s * 1e6, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+        },
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(line), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -14,8 +14,6 @@
  *   msgl_paged_decode        attention/metal.py:112-131   paged_decode_attention
  *                            (semantics of attention/naive.py:50-60 forward_decode)
  *   msgl_prefill_ragged      attention/base.py:85-105     BaseAttnBackend._forward_prefill
- *   msgl_build_decode_meta   attention/metal.py:145-152   MetalAttnBackend.prepare_decode
- *                            + scheduler/scheduler.py:154-157 (out_loc, positions)
  *
  * Layouts (identical to the reference, no transposes at the boundary):
  *   q, out   [T, Hq, D]   row-major, dtype `dtype`
@@ -94,6 +92,29 @@ int msgl_paged_decode(const void* q, const void* k_pool, const void* v_pool, con
                       int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                       int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Ragged chunked-prefill attention over a paged pool, one launch per batch.
+ * Replaces attention/base.py:85-105 (BaseAttnBackend._forward_prefill, a
+ * per-request MLX SDPA loop).
+ *
+ *   q          [T, Hq, D] packed extend tokens; request i owns rows
+ *              q_indptr[i] .. q_indptr[i+1]-1 (E_i rows)
+ *   kv_indptr  offsets into kv_indices ([R+1]; with seq_lens only [R] read)
+ *   kv_indices slots (page ids when page_size > 1) of request i's full KV:
+ *              the cached prefix followed by this step's E_i rows, which the
+ *              caller stored with msgl_store_kv first
+ *   seq_lens   [R] L_i = P_i + E_i, or NULL (L_i = kv_indptr[i+1]-kv_indptr[i])
+ *   max_extend_len  max_i E_i (sizes the grid)
+ *   out        [T, Hq, D]
+ * Query t of request i sees keys j <= P_i + t (MLX's bottom-right causal
+ * mask, docs/04-attention.md:35-36); E_i <= L_i is required.
+ */
+int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, const int32_t* q_indptr,
+                        const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                        int32_t num_reqs, int32_t max_extend_len, int32_t num_qo_heads, int32_t num_kv_heads,
+                        int32_t head_dim, int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                        void* out, void* stream);
 
 #ifdef __cplusplus
 }

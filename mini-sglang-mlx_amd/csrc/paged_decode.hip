@@ -421,7 +421,7 @@ extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* 
                                  void* workspace, int64_t workspace_bytes, void* stream) {
   using namespace msgl;
   clear_error();
-  MSGL_CHECK_ARG(batch >= 0, "msgl_paged_decode: batch must be >= 0");
+  MSGL_CHECK_ARG(batch >= 0 && batch <= 65535, "msgl_paged_decode: batch must be in [0, 65535]");
   if (batch == 0) return MSGL_OK;
   MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "msgl_paged_decode: sizes must be > 0");
   MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "msgl_paged_decode: Hq (%d) must be a multiple of Hkv (%d)",

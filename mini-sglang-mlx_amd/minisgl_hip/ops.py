@@ -125,3 +125,64 @@ def paged_decode_attention(
     )
     _lib.check(status, "msgl_paged_decode")
     return out
+
+
+def prefill_ragged_attention(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    q_indptr: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    kv_indices: torch.Tensor,
+    seq_lens: Optional[torch.Tensor],
+    scale: Union[float, torch.Tensor],
+    *,
+    max_extend_len: int,
+    page_size: int = 1,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Ragged prefill over cached prefixes; counterpart of attention/base.py:85-105.
+
+    q [T, Hq, D] packed; request i owns q rows q_indptr[i]:q_indptr[i+1] and
+    attends (bottom-right causal) to the first seq_lens[i] tokens of its KV at
+    kv_indices[kv_indptr[i]:] (token slots, or page ids when page_size > 1).
+    ``max_extend_len`` must bound every request's extend length (host-known).
+    """
+    if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
+        raise ValueError("q must be [T, Hq, D] and pools [N, Hkv, D]")
+    t, hq, d = q.shape
+    n_slots, hkv, dk = k_pool.shape
+    if dk != d or hq % hkv != 0:
+        raise ValueError(f"head_dim mismatch or Hq ({hq}) not a multiple of Hkv ({hkv})")
+    if len({q.dtype, k_pool.dtype, v_pool.dtype}) != 1:
+        raise ValueError("q and pools must share one dtype")
+    if page_size > 1 and seq_lens is None:
+        raise ValueError("page_size > 1 needs seq_lens")
+    if q_indptr.dim() != 1 or q_indptr.shape[0] < 2:
+        raise ValueError("q_indptr must be [R+1]")
+    num_reqs = q_indptr.shape[0] - 1
+    dev = q.device
+    for name, x in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _check_device(name, x, dev)
+    for name, x in (("q_indptr", q_indptr), ("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
+                    ("seq_lens", seq_lens)):
+        _check_index(name, x, dev)
+    if isinstance(scale, torch.Tensor):
+        scale = float(scale.reshape(-1)[0].item())
+    if out is None:
+        out = torch.empty_like(q)
+    else:
+        _check_device("out", out, dev)
+        if out.shape != q.shape or out.dtype != q.dtype:
+            raise ValueError("out must match q's shape and dtype")
+    if t == 0:
+        return out
+    lib = _lib.load()
+    status = lib.msgl_prefill_ragged(
+        _lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool),
+        _lib.ptr(q_indptr), _lib.ptr(kv_indptr), _lib.ptr(kv_indices), _lib.ptr(seq_lens),
+        num_reqs, int(max_extend_len), hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
+        _lib.ptr(out), _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_prefill_ragged")
+    return out

@@ -66,3 +66,55 @@ def test_decode_steps_through_backend(cuda_device):
             assert torch.equal(kv.k[layer][batch.out_loc.long()], k)
         for r in reqs:
             r.complete_one()
+
+
+def test_prefill_then_decode_through_backend(cuda_device):
+    """Chunked prefill (one request with a cached prefix, one without) followed
+    by a decode step, all through prepare_metadata / store_kv / forward."""
+    dt = torch.bfloat16
+    cfg, kv, table, backend = _setup(cuda_device, dt, num_layers=2)
+    rng = np.random.default_rng(1)
+    free = rng.permutation(8192).astype(np.int32)
+    # request A: 50-token prompt whose first 20 tokens are already cached
+    # request B: 33-token prompt, nothing cached
+    reqs = [Req(input_ids=np.zeros(50, np.int32), table_idx=0, cached_len=20),
+            Req(input_ids=np.zeros(33, np.int32), table_idx=5, cached_len=0)]
+    free = oracle.allocate_paged(table, free, [0], [0], [20], 1)  # the cached prefix's slots
+    for layer in range(cfg.num_layers):
+        kv.k[layer].copy_(randn(kv.k[layer].shape, 40 + layer, dt).to(cuda_device))
+        kv.v[layer].copy_(randn(kv.v[layer].shape, 50 + layer, dt).to(cuda_device))
+    for phase in ("prefill", "decode"):
+        rows = [r.table_idx for r in reqs]
+        cached = [r.cached_len for r in reqs]
+        device = [r.device_len for r in reqs]
+        free = oracle.allocate_paged(table, free, rows, cached, device, 1)
+        pos, out_loc = oracle.prepare_batch_indices(table, rows, cached, device)
+        batch = Batch(reqs=reqs, phase=phase)
+        batch.positions = i32(pos, cuda_device)
+        batch.out_loc = i32(out_loc, cuda_device)
+        backend.prepare_metadata(batch)
+        if phase == "prefill":
+            q_off, last, kvi = oracle.prefill_metadata(table, rows, cached, device)
+            assert batch.attn_metadata.q_offsets == q_off
+            assert np.array_equal(batch.attn_metadata.last_indices.cpu().numpy(), last)
+            assert batch.attn_metadata.kv_indices[1] is None
+            assert np.array_equal(batch.attn_metadata.kv_indices[0], kvi[0])
+        t = len(out_loc)
+        for layer in range(cfg.num_layers):
+            q = randn((t, 16, 128), 60 + layer, dt).to(cuda_device)
+            k = randn((t, 8, 128), 70 + layer, dt).to(cuda_device)
+            v = randn((t, 8, 128), 80 + layer, dt).to(cuda_device)
+            print(f"case backend {phase} layer={layer}", flush=True)
+            kv.store_kv(k, v, batch.out_loc, layer)
+            o = backend.forward(q, k, v, layer, batch)
+            torch.cuda.synchronize()
+            kp, vp = to_np64(kv.k[layer]), to_np64(kv.v[layer])
+            if phase == "prefill":
+                ref = oracle.forward_prefill(to_np64(q), to_np64(k), to_np64(v), kp, vp, q_off, kvi,
+                                             cfg.head_dim**-0.5)
+            else:
+                kvi_d, mask = oracle.naive_decode_metadata(table, rows, device)
+                ref = oracle.naive_forward_decode(to_np64(q), kp, vp, kvi_d, mask, cfg.head_dim**-0.5)
+            assert_close(o, ref, dt, f"backend {phase} layer {layer}")
+        for r in reqs:
+            r.complete_one()

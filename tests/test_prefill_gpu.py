@@ -1,0 +1,96 @@
+"""Ragged chunked prefill on the GPU vs the float64 oracle (attention/base.py:85-105,
+bottom-right causal over a cached prefix)."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import DTYPES, assert_close, i32, randn, to_np64
+from minisgl_hip import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+
+def _run(case, hq, hkv, d, dt, device, seed, page_size=1):
+    n = case.num_slots
+    kp = randn((n, hkv, d), seed, dt).to(device)
+    vp = randn((n, hkv, d), seed + 1, dt).to(device)
+    q = randn((case.num_tokens, hq, d), seed + 2, dt).to(device)
+    knew = randn((case.num_tokens, hkv, d), seed + 3, dt).to(device)
+    vnew = randn((case.num_tokens, hkv, d), seed + 4, dt).to(device)
+    ops.store_kv(knew, vnew, i32(case.out_loc, device), kp, vp)
+    if page_size == 1:
+        kv_indptr, kv_indices, seq = case.kv_indptr, case.kv_indices, None
+    else:
+        pages = []
+        for i, L in enumerate(case.seq_lens):
+            row = case.page_table[i, : int(L)]
+            pages.append(row[::page_size] // page_size)
+        kv_indptr = np.concatenate([[0], np.cumsum([len(x) for x in pages])]).astype(np.int32)
+        kv_indices = np.concatenate(pages).astype(np.int32)
+        seq = case.seq_lens
+    out = ops.prefill_ragged_attention(
+        q, kp, vp, i32(case.q_indptr, device), i32(kv_indptr, device), i32(kv_indices, device),
+        None if seq is None else i32(seq, device), d**-0.5,
+        max_extend_len=int(case.extend_lens.max()), page_size=page_size,
+    )
+    torch.cuda.synchronize()
+    return q, knew, vnew, kp, vp, out
+
+
+def _oracle(case, q, knew, vnew, kp, vp, d, rows=None):
+    kvi = [None if case.prefix_lens[i] == 0 else case.kv_indices[case.kv_indptr[i] : case.kv_indptr[i + 1]]
+           for i in range(len(case.seq_lens))]
+    if rows is None:
+        return oracle.forward_prefill(to_np64(q), to_np64(knew), to_np64(vnew), to_np64(kp), to_np64(vp),
+                                      case.q_indptr.tolist(), kvi, d**-0.5)
+    outs = []
+    for i in rows:
+        s, e = int(case.q_indptr[i]), int(case.q_indptr[i + 1])
+        slots = torch.from_numpy(case.kv_indices[case.kv_indptr[i] : case.kv_indptr[i + 1]].astype(np.int64))
+        kb = to_np64(kp.index_select(0, slots.to(kp.device)))
+        vb = to_np64(vp.index_select(0, slots.to(vp.device)))
+        outs.append(oracle.forward_prefill(to_np64(q[s:e]), None, None, kb, vb, [0, e - s],
+                                           [np.arange(len(slots))], d**-0.5))
+    return np.concatenate(outs)
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256)])
+def test_prefill_grid(cuda_device, hq, hkv, d, dtype):
+    """Prefix P in {0,1,17,300,0}, extend E in {1,2,64,100,37}: causal edges, E == 1, P == 0."""
+    dt = DTYPES[dtype]
+    case = workloads.prefill_case_from_lens([0, 1, 17, 300, 0], [1, 2, 64, 100, 37], num_slots=2048, seed=3)
+    print(f"case prefill grid {hq}/{hkv}/{d} {dtype}", flush=True)
+    q, kn, vn, kp, vp, out = _run(case, hq, hkv, d, dt, cuda_device, 10)
+    ref = _oracle(case, q, kn, vn, kp, vp, d)
+    assert_close(out, ref, dt, f"prefill {hq}/{hkv}/{d} {dtype}")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+def test_prefill_page_size_16(cuda_device, dtype):
+    dt = DTYPES[dtype]
+    case = workloads.prefill_case_from_lens([0, 15, 16, 40, 333], [5, 1, 33, 100, 64], num_slots=8192, page_size=16,
+                                            seed=4)
+    print(f"case prefill page16 {dtype}", flush=True)
+    q, kn, vn, kp, vp, out = _run(case, 32, 8, 128, dt, cuda_device, 20, page_size=16)
+    ref = _oracle(case, q, kn, vn, kp, vp, 128)
+    assert_close(out, ref, dt, f"prefill page16 {dtype}")
+
+
+def test_prefill_cfg4_sampled(cuda_device):
+    """16 requests, P ~ U[0,4096], E ~ U[64,512] rescaled to <= 2048 packed tokens, bf16."""
+    case = workloads.prefill_case(16, 4096, 64, 512, 2048, num_slots=1 << 17, seed=0)
+    print("case prefill cfg4", flush=True)
+    q, kn, vn, kp, vp, out = _run(case, 16, 8, 128, torch.bfloat16, cuda_device, 30)
+    rows = [0, 3, 7, 15]
+    ref = _oracle(case, q, kn, vn, kp, vp, 128, rows=rows)
+    sel = np.concatenate([np.arange(case.q_indptr[i], case.q_indptr[i + 1]) for i in rows])
+    assert_close(out[torch.from_numpy(sel).to(cuda_device)], ref, torch.bfloat16, "cfg4 sampled")
+    out2 = ops.prefill_ragged_attention(
+        q, kp, vp, i32(case.q_indptr, cuda_device), i32(case.kv_indptr, cuda_device),
+        i32(case.kv_indices, cuda_device), None, 128**-0.5, max_extend_len=int(case.extend_lens.max()),
+    )
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "prefill is not deterministic"
