@@ -131,7 +131,7 @@ def main():
     indices = torch.from_numpy(c.kv_indices).to(dev)
     out_loc = torch.from_numpy(c.out_loc).to(dev)
     splits = args.splits or ops.default_splits(BATCH, HKV, int(c.lens.max()))
-    ws = torch.empty(max(1, ops.decode_workspace_bytes(BATCH, HQ, D, splits)), dtype=torch.uint8, device=dev)
+    ws = ops.decode_workspace(BATCH, HQ, HKV, D, splits, dev)
     scale = D**-0.5
 
     def step(events=None):

@@ -63,9 +63,14 @@ int msgl_store_kv(const void* k, const void* v, const int32_t* out_loc, void* k_
 /* Default split count for msgl_paged_decode (max_splits <= 0 picks this). */
 int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len);
 
-/* Bytes of workspace msgl_paged_decode needs for these sizes. */
-int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
-                                         int32_t max_splits);
+/*
+ * Bytes of workspace msgl_paged_decode needs for these sizes (0 when
+ * max_splits <= 1): fp32 split-K partials (m, l and the unnormalised output
+ * per chunk and query head). Its contents need no initialisation. Calls that
+ * overlap in time must not share a workspace; calls in order on one stream may.
+ */
+int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                         int32_t head_dim, int32_t max_splits);
 
 /*
  * Paged decode attention, one query token per request.
@@ -83,7 +88,9 @@ int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, in
  *   scale      softmax scale (attention/base.py:45: head_dim ** -0.5)
  *   max_splits split-K factor bound (<= 0: msgl_paged_decode_default_splits)
  *   out        [B, Hq, D]
- *   workspace  >= msgl_paged_decode_workspace_size(B, Hq, D, max_splits) bytes
+ *   workspace  >= msgl_paged_decode_workspace_size(B, Hq, Hkv, D, max_splits)
+ *              bytes, 256-byte aligned
+ * Launches the decode kernel and, when max_splits > 1, the split-K merge.
  * A request with L_b == 0 gets a zero output row. Slots outside
  * [0, num_slots) are clamped to slot 0 (memory-safe; result unspecified).
  */

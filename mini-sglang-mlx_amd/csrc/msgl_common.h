@@ -121,6 +121,10 @@ __device__ __forceinline__ float to_f32<f16_t>(f16_t x) { return (float)x; }
 
 // 16-byte global load / store (dwordx4).
 __device__ __forceinline__ u32x4 ld16(const void* p) { return *reinterpret_cast<const u32x4*>(p); }
+// Streaming 16-byte load for data read exactly once (nontemporal cache policy).
+__device__ __forceinline__ u32x4 ld16_stream(const void* p) {
+  return __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+}
 __device__ __forceinline__ void st16(void* p, const u32x4& v) { *reinterpret_cast<u32x4*>(p) = v; }
 
 // ---------------------------------------------------------------------------

@@ -5,31 +5,46 @@
 //   o[b, h] = softmax_j(scale * q[b,h] . K[slot_b(j), h/G]) V[slot_b(j), h/G],  j < L_b
 //
 // Design (MI355X-first, not a translation of the Metal kernel):
-//  * Work unit = one wavefront per (request b, split s, kv head). A workgroup
-//    holds the Hkv wavefronts of one (b, s), so the rows of a token slot
-//    (Hkv * D contiguous elements) are read by neighbouring waves together.
+//  * Work unit = one wavefront per (request b, split s, kv head). Workgroups
+//    are small (one wavefront by default) so a CU refills as soon as any unit
+//    finishes; the kv heads of one (b, s) are neighbouring workgroups, so the
+//    rows of a slot (Hkv * D contiguous elements) are read close in time. A
+//    workgroup gathers its token slots once into LDS.
 //  * Split-K: request b is cut into n_b <= max_splits chunks of a multiple of
-//    16 tokens (>= kMinChunk), decided on the device from L_b alone, so the
-//    launch needs no host-side lengths. Single-chunk requests write the final
-//    row; others write fp32 partials (acc, m, l) merged by a second kernel.
+//    16 tokens (>= kMinChunk), decided on the device from L_b alone. A
+//    single-chunk request writes its final row. Otherwise every chunk writes
+//    fp32 partials (acc, m, l) and a merge kernel with one wavefront per
+//    (request, kv head) combines them. (Merging inside the decode launch
+//    needs a device-scope release per chunk, which on this part writes back
+//    the XCD's L2 each time and costs far more than a second launch.)
 //  * Q.K^T runs on the matrix cores: v_mfma_f32_16x16x32_{bf16,f16} (or
 //    16x16x4 f32), A = the G query heads of the kv head (rows >= G are zero),
-//    B = 16 K rows straight from the pool (one 16-byte load per lane per MFMA,
-//    no conversion). Output: lane (t = l%16, row group l/16) holds 4 scores.
+//    B = 16 K rows (no conversion). Output: lane (t = l%16, row group l/16)
+//    holds 4 scores. K rows are fetched like V rows -- each 16-lane group reads
+//    one whole row -- and re-laid into the B layout through a padded per-wave
+//    LDS tile: on MI355X a load instruction spanning 4 rows x 256 B streams far
+//    faster than one spanning 16 rows x 64 B (the B layout's own shape).
 //  * Online softmax in the exp2 domain (scale*log2(e) folded into the score)
-//    with the tile max over the 16 tokens from 4 DPP steps inside a 16-lane row.
+//    with the tile max over 16 tokens from 4 DPP steps inside a 16-lane row;
+//    only the MFMA rows that hold query heads are processed.
 //  * P.V on the VALU: lane (token sub-row, 16-byte d chunk) accumulates
 //    G x (16/sizeof T) fp32 outputs; P and the rescale factors go through a
-//    1 KiB per-wave LDS tile. Partial sums over token sub-rows are folded once
-//    per work unit.
-//  * Slot indices: one coalesced load of 64 slots per 64 tokens, handed to the
-//    lanes that need them with ds_bpermute; out-of-range slots are clamped.
+//    small per-wave LDS tile.
+//  * The tile loop is software pipelined: the K/V loads of the next NST-1
+//    tiles are in flight (a ring of register buffers) while one tile is
+//    computed, which is what it takes to keep ~200 KiB of loads in flight per
+//    CU at 2 wavefronts per SIMD. K/V rows
+//    are read exactly once per launch, so they use nontemporal (streaming)
+//    loads, which sustain markedly more HBM bandwidth for random row gathers
+//    on MI355X than default-policy loads.
 #include "msgl_common.h"
 
 namespace msgl {
 
 constexpr int kMinChunk = 64;   // smallest split-K chunk (tokens)
-constexpr int kMaxSplits = 64;  // merge kernel's LDS bound
+constexpr int kMaxSplits = 64;  // bound on splits per request
+constexpr int kSeg = 512;       // token slots staged in LDS at a time
+constexpr int kSlotPad = 16 * 7;  // room for up to 7 padding tiles of prefetch
 constexpr float kLog2e = 1.4426950408889634f;
 
 // ---- per-dtype matrix-core step for S = Q K^T over one 16-byte chunk ------
@@ -65,7 +80,7 @@ struct QK<float> {
   }
 };
 
-// Split geometry of one request; identical in the decode and merge kernels.
+// Split geometry of one request.
 __device__ __forceinline__ void split_geometry(int L, int max_splits, int& n, int& chunk) {
   if (L <= 0) {
     n = 0;
@@ -79,15 +94,15 @@ __device__ __forceinline__ void split_geometry(int L, int max_splits, int& n, in
   n = (L + chunk - 1) / chunk;
 }
 
-__device__ __forceinline__ int64_t slot_of(const int32_t* __restrict__ kv_indices, int start, int tok, int page_size,
-                                           int64_t num_slots) {
+__device__ __forceinline__ int slot_of(const int32_t* __restrict__ kv_indices, int start, int tok, int page_size,
+                                       int64_t num_slots) {
   int64_t s;
   if (page_size == 1) {
     s = kv_indices[start + tok];
   } else {
     s = (int64_t)kv_indices[start + tok / page_size] * page_size + tok % page_size;
   }
-  return (s >= 0 && s < num_slots) ? s : 0;
+  return (s >= 0 && s < num_slots) ? (int)s : 0;
 }
 
 struct DecodeParams {
@@ -98,8 +113,8 @@ struct DecodeParams {
   const int32_t* kv_indices;
   const int32_t* seq_lens;
   void* out;
-  float* part_o;   // [B, S, Hq, D]
-  float* part_ml;  // [B, S, Hq, 2]
+  float* part_ml;     // [B, S, Hq, 2]
+  float* part_o;      // [B, S, Hq, D]
   int64_t num_slots;
   int hq, hkv, page_size, max_splits;
   float scale_log2;
@@ -108,8 +123,33 @@ struct DecodeParams {
 // LDS per wavefront: P tile [16 tokens][16 rows] + alpha[16] + (m, l)[16 rows].
 constexpr int kLdsPerWave = 16 * 16 + 16 + 32;
 
+// One 16-token tile of K and V rows as loaded: both in row layout (LPR
+// consecutive lanes read one whole row, R rows per instruction).
+template <typename T, int D>
+struct TileBuf {
+  static constexpr int VEC = QK<T>::VEC;
+  static constexpr int NL = 16 / (64 / (D / VEC));
+  u32x4 k[NL];
+  u32x4 v[NL];
+};
+
+// Per-wave LDS K tile: 16 rows of D elements, row stride padded by 16 bytes so
+// row-wise writes and 16-row column reads are both free of bank conflicts.
+template <typename T, int D>
+constexpr int k_lds_stride() { return D * (int)sizeof(T) + 16; }
+
+// Minimum wavefronts per SIMD the register allocator must allow (occupancy).
+#ifndef MSGL_DECODE_MIN_WAVES
+#define MSGL_DECODE_MIN_WAVES 2
+#endif
+// Tiles of K/V held in registers per wavefront (1 computing + NST-1 in flight).
+#ifndef MSGL_DECODE_STAGES
+#define MSGL_DECODE_STAGES 2
+#endif
+
 template <typename T, int D, int G>
-__global__ __launch_bounds__(512) void paged_decode_kernel(DecodeParams p) {
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(MSGL_DECODE_MIN_WAVES)))
+void paged_decode_kernel(DecodeParams p) {
   constexpr int VEC = QK<T>::VEC;   // elements per 16-byte chunk
   constexpr int ES = sizeof(T);
   constexpr int KCHUNK = 4 * VEC;   // d covered by one K load across the 4 row groups
@@ -117,63 +157,70 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(DecodeParams p) {
   constexpr int LPR = D / VEC;      // lanes per V row
   constexpr int R = 64 / LPR;       // V rows per wave load
   constexpr int NLV = 16 / R;       // V loads per lane per tile
+  constexpr int NR = G < 4 ? G : 4; // MFMA accumulator rows holding query heads
+  constexpr int NST = (sizeof(T) == 4 || D > 128 || G > 4) ? 2 : MSGL_DECODE_STAGES;  // register budget
+  static_assert(NST >= 2 && (NST - 1) * 16 <= kSlotPad, "pipeline depth");
   static_assert(D % KCHUNK == 0 && 64 % LPR == 0 && 16 % R == 0, "unsupported head_dim");
   static_assert(G >= 1 && G <= 16, "unsupported group size");
 
   extern __shared__ float lds_all[];
+  int* slots_lds = reinterpret_cast<int*>(lds_all);  // [kSeg + kSlotPad]
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nwaves = blockDim.x >> 6;
-  float* lds = lds_all + wave * kLdsPerWave;
+  constexpr int KRS = k_lds_stride<T, D>();
+  float* lds = lds_all + kSeg + kSlotPad + wave * (kLdsPerWave + 16 * KRS / 4);
   float* P_lds = lds;              // [16][16]
   float* A_lds = lds + 256;        // [16]
   float* ML_lds = lds + 256 + 16;  // [16][2]
+  uint8_t* K_lds = reinterpret_cast<uint8_t*>(lds + kLdsPerWave);  // [16][KRS bytes]
 
+  // grid.x = split * kv-head groups + group; a group is this workgroup's waves
+  const int ngrp = (p.hkv + nwaves - 1) / nwaves;
   const int b = blockIdx.y;
-  const int split = blockIdx.x;
-  int start, L;
-  if (p.seq_lens) {
-    start = p.kv_indptr[b];
-    L = p.seq_lens[b];
-  } else {
-    start = p.kv_indptr[b];
-    L = p.kv_indptr[b + 1] - start;
-  }
+  const int split = blockIdx.x / ngrp;
+  const int kgrp = blockIdx.x % ngrp;
+  const int start = p.kv_indptr[b];
+  const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - start;
   int n, chunk;
   split_geometry(L, p.max_splits, n, chunk);
   if (split >= n) {
-    if (split == 0) {  // L == 0: defined zero output
+    if (split == 0) {  // L == 0: defined zero output for this group's heads
+      const int h0 = kgrp * nwaves * G;
+      const int h1 = min(p.hq, h0 + nwaves * G);
       T* o = reinterpret_cast<T*>(p.out) + (int64_t)b * p.hq * D;
-      for (int i = threadIdx.x; i < p.hq * D; i += blockDim.x) o[i] = from_f32<T>(0.f);
+      for (int i = h0 * D + threadIdx.x; i < h1 * D; i += blockDim.x) o[i] = from_f32<T>(0.f);
     }
     return;
   }
   const int t0 = split * chunk;
   const int t1 = min(L, t0 + chunk);
 
-  const int r = lane & 15;  // MFMA column (token in tile) / A row
-  const int g4 = lane >> 4;  // MFMA row group
+  const int r = lane & 15;    // MFMA column (token in tile) / A row
+  const int g4 = lane >> 4;   // MFMA row group
   const int vc = lane % LPR;  // V: 16-byte chunk within the row
   const int vr = lane / LPR;  // V: token sub-row
 
-  const uint8_t* kp = reinterpret_cast<const uint8_t*>(p.k_pool);
-  const uint8_t* vp = reinterpret_cast<const uint8_t*>(p.v_pool);
   const int64_t row_stride = (int64_t)p.hkv * D * ES;  // bytes per slot
 
-  for (int kvh = wave; kvh < p.hkv; kvh += nwaves) {
+  {
+    const int kvh = kgrp * nwaves + wave;
+    const bool active = kvh < p.hkv;
+    const int kvh_c = active ? kvh : 0;
+
     // Q fragment: A operand, row r = query head kvh*G + r (zero when r >= G).
     u32x4 qa[NLK];
     {
       const uint8_t* qrow =
-          reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)b * p.hq + kvh * G + r) * D * ES + g4 * VEC * ES;
+          reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)b * p.hq + kvh_c * G + r) * D * ES + g4 * VEC * ES;
 #pragma unroll
       for (int j = 0; j < NLK; ++j) {
         qa[j] = (r < G) ? ld16(qrow + j * KCHUNK * ES) : u32x4{0u, 0u, 0u, 0u};
       }
     }
-    float m_run[4], l_run[4];
+    float m_run[NR], l_run[NR];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
+    for (int i = 0; i < NR; ++i) {
       m_run[i] = -INFINITY;
       l_run[i] = 0.f;
     }
@@ -183,41 +230,52 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(DecodeParams p) {
 #pragma unroll
       for (int e = 0; e < VEC; ++e) acc[g][e] = 0.f;
 
-    const int64_t head_off = (int64_t)kvh * D * ES;
+    const uint8_t* kbase_p = reinterpret_cast<const uint8_t*>(p.k_pool) + (int64_t)kvh_c * D * ES + vc * VEC * ES;
+    const uint8_t* vbase_p = reinterpret_cast<const uint8_t*>(p.v_pool) + (int64_t)kvh_c * D * ES + vc * VEC * ES;
 
-    for (int tb = t0; tb < t1; tb += 64) {
-      const int my_tok = tb + lane;
-      const int64_t my_slot = (my_tok < t1) ? slot_of(p.kv_indices, start, my_tok, p.page_size, p.num_slots) : 0;
-      const int my_slot32 = (int)my_slot;  // slots < 2^31 (checked on the host)
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const int tt = tb + 16 * k;
-        if (tt >= t1) break;
-        // ---- loads: K rows for the MFMA, V rows for the PV lanes ----
-        const int ks = __shfl(my_slot32, 16 * k + r);
-        u32x4 kb[NLK];
-        {
-          const uint8_t* krow = kp + (int64_t)ks * row_stride + head_off + g4 * VEC * ES;
-#pragma unroll
-          for (int j = 0; j < NLK; ++j) kb[j] = ld16(krow + j * KCHUNK * ES);
-        }
-        u32x4 vb[NLV];
+    for (int s0 = t0; s0 < t1; s0 += kSeg) {
+      const int seg_len = min(kSeg, t1 - s0);
+      const int ntile = (seg_len + 15) >> 4;
+      // ---- stage this segment's slots, padded by NST-1 tiles; positions past
+      //      the end repeat the last valid slot ----
+      __syncthreads();
+      for (int i = threadIdx.x; i < (ntile + NST - 1) * 16; i += blockDim.x) {
+        const int tok = s0 + min(i, seg_len - 1);
+        slots_lds[i] = slot_of(p.kv_indices, start, tok, p.page_size, p.num_slots);
+      }
+      __syncthreads();
+      if (!active) continue;
+
+      // Prefetches past the segment end read the padded slot list (the last
+      // valid slot, one row per tile, already fetched): every path through the
+      // loop keeps the same loads in flight, so the compiler waits for exactly
+      // one tile instead of draining the pipeline at each branch.
+      auto issue = [&](TileBuf<T, D>& buf, int tile) {
+        const int base = tile * 16;
 #pragma unroll
         for (int i = 0; i < NLV; ++i) {
-          const int tl = vr + R * i;
-          const int vs = __shfl(my_slot32, 16 * k + tl);
-          const u32x4 x = ld16(vp + (int64_t)vs * row_stride + head_off + vc * VEC * ES);
-          vb[i] = (tt + tl < t1) ? x : u32x4{0u, 0u, 0u, 0u};
+          const int64_t off = (int64_t)slots_lds[base + vr + R * i] * row_stride;
+          buf.k[i] = ld16_stream(kbase_p + off);
+          buf.v[i] = ld16_stream(vbase_p + off);
         }
-        // ---- S = Q K^T on the matrix core ----
+      };
+
+      auto compute = [&](const TileBuf<T, D>& buf, int tile) {
+        // K rows -> LDS -> MFMA B layout (lane: token r, d chunk j*KCHUNK + g4*VEC)
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < NLV; ++i) *reinterpret_cast<u32x4*>(K_lds + (vr + R * i) * KRS + vc * 16) = buf.k[i];
+        wave_lds_sync();
+        // S = Q K^T on the matrix core
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < NLK; ++j) s = QK<T>::step(qa[j], kb[j], s);
-        // ---- online softmax (exp2 domain) ----
-        const bool valid = (tt + r) < t1;
-        float pr[4], al[4];
+        for (int j = 0; j < NLK; ++j)
+          s = QK<T>::step(qa[j], *reinterpret_cast<const u32x4*>(K_lds + r * KRS + (j * KCHUNK + g4 * VEC) * ES), s);
+        // online softmax (exp2 domain)
+        const bool valid = tile * 16 + r < seg_len;
+        float pr[4] = {0.f, 0.f, 0.f, 0.f}, al[4] = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
+        for (int i = 0; i < NR; ++i) {
           const float x = valid ? s[i] * p.scale_log2 : -INFINITY;
           const float mt = row16_max(x);
           const float m_new = fmaxf(m_run[i], mt);
@@ -230,7 +288,7 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(DecodeParams p) {
         *reinterpret_cast<f32x4*>(P_lds + r * 16 + 4 * g4) = f32x4{pr[0], pr[1], pr[2], pr[3]};
         if (r == 0) *reinterpret_cast<f32x4*>(A_lds + 4 * g4) = f32x4{al[0], al[1], al[2], al[3]};
         wave_lds_sync();
-        // ---- O = alpha * O + P V on the VALU ----
+        // O = alpha * O + P V on the VALU
         float alpha[G];
 #pragma unroll
         for (int g = 0; g < G; ++g) alpha[g] = A_lds[g];
@@ -242,7 +300,7 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(DecodeParams p) {
         for (int i = 0; i < NLV; ++i) {
           const int tl = vr + R * i;
           float vf[VEC];
-          Vec16<T>::to_f32(vb[i], vf);
+          Vec16<T>::to_f32(buf.v[i], vf);
           float pv[G];
 #pragma unroll
           for (int g = 0; g < G; ++g) pv[g] = P_lds[tl * 16 + g];
@@ -251,12 +309,27 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(DecodeParams p) {
 #pragma unroll
             for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pv[g], vf[e], acc[g][e]);
         }
+      };
+
+      // NST-stage register pipeline: tiles t+1 .. t+NST-1 are in flight while t computes
+      TileBuf<T, D> buf[NST];
+#pragma unroll
+      for (int i = 0; i < NST - 1; ++i) issue(buf[i], i);  // tiles past ntile are padding
+      for (int tile = 0; tile < ntile; tile += NST) {
+#pragma unroll
+        for (int k = 0; k < NST; ++k) {
+          const int t = tile + k;
+          if (t >= ntile) break;
+          issue(buf[(k + NST - 1) % NST], t + NST - 1);
+          compute(buf[k], t);
+        }
       }
     }
+    if (!active) return;
 
     // ---- fold: l over the 16 token lanes, acc over the R token sub-rows ----
 #pragma unroll
-    for (int i = 0; i < 4; ++i) l_run[i] = row16_sum(l_run[i]);
+    for (int i = 0; i < NR; ++i) l_run[i] = row16_sum(l_run[i]);
 #pragma unroll
     for (int off = LPR; off < 64; off <<= 1)
 #pragma unroll
@@ -266,15 +339,15 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(DecodeParams p) {
     wave_lds_sync();
     if (r == 0) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
+      for (int i = 0; i < NR; ++i) {
         ML_lds[(4 * g4 + i) * 2 + 0] = m_run[i];
         ML_lds[(4 * g4 + i) * 2 + 1] = l_run[i];
       }
     }
     wave_lds_sync();
-    if (lane < LPR) {
-      const int d0 = vc * VEC;
-      if (n == 1) {
+    const int d0 = vc * VEC;
+    if (n == 1) {
+      if (lane < LPR) {
         T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D + d0;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
@@ -286,76 +359,90 @@ __global__ __launch_bounds__(512) void paged_decode_kernel(DecodeParams p) {
           __builtin_memcpy(&packed, tmp, 16);
           st16(o + g * D, packed);
         }
-      } else {
-        const int64_t base = ((int64_t)b * p.max_splits + split) * p.hq + kvh * G;
-#pragma unroll
-        for (int g = 0; g < G; ++g) {
-          float* po = p.part_o + (base + g) * D + d0;
-#pragma unroll
-          for (int e = 0; e < VEC; e += 4)
-            *reinterpret_cast<f32x4*>(po + e) = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
-          if (vc == 0) {
-            p.part_ml[(base + g) * 2 + 0] = ML_lds[g * 2 + 0];
-            p.part_ml[(base + g) * 2 + 1] = ML_lds[g * 2 + 1];
-          }
-        }
       }
+      return;
+    }
+
+    // ---- split-K: publish this chunk's partials for the merge kernel ----
+    const int64_t base = ((int64_t)b * p.max_splits + split) * p.hq + kvh * G;
+    if (lane < LPR) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float* po = p.part_o + (base + g) * D + d0;
+#pragma unroll
+        for (int e = 0; e < VEC; e += 4)
+          *reinterpret_cast<f32x4*>(po + e) = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
+      }
+    }
+    if (lane < G) {
+      p.part_ml[(base + lane) * 2 + 0] = ML_lds[lane * 2 + 0];
+      p.part_ml[(base + lane) * 2 + 1] = ML_lds[lane * 2 + 1];
     }
   }
 }
 
-// Merge split-K partials: o = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
-// (the same combine as the Metal kernel's simdgroup merge, attention/metal.py:75-94).
-template <typename T, int D>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p) {
-  __shared__ float w[kMaxSplits * 64];  // [Hq (<= 64)][splits] weights
-  const int b = blockIdx.x;
-  int L;
-  if (p.seq_lens) {
-    L = p.seq_lens[b];
-  } else {
-    L = p.kv_indptr[b + 1] - p.kv_indptr[b];
-  }
+// Merge split-K partials, one wavefront per (request, kv head):
+//   o = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
+// (the combine of the Metal kernel's simdgroup merge, attention/metal.py:75-94).
+// Lanes own float4 chunks of the G*D outputs; every split's loads are
+// independent, so a wavefront keeps all of them in flight.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p, int batch) {
+  const int unit = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // (b, kvh)
+  const int lane = threadIdx.x & 63;
+  if (unit >= batch * p.hkv) return;
+  const int b = unit / p.hkv, kvh = unit % p.hkv;
+  const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];
   int n, chunk;
   split_geometry(L, p.max_splits, n, chunk);
   if (n <= 1) return;
-  const int64_t base = (int64_t)b * p.max_splits * p.hq;
-  for (int h = threadIdx.x; h < p.hq; h += blockDim.x) {
+  const int64_t bbase = (int64_t)b * p.max_splits * p.hq + kvh * G;
+  constexpr int C4 = D / 4;
+  T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D;
+  for (int c = lane; c < G * C4; c += 64) {
+    const int g = c / C4, d4 = c % C4;
+    const float* ml = p.part_ml + (bbase + g) * 2;
+    const int64_t mstride = (int64_t)p.hq * 2;
     float M = -INFINITY;
-    for (int s = 0; s < n; ++s) M = fmaxf(M, p.part_ml[(base + (int64_t)s * p.hq + h) * 2]);
+    for (int s = 0; s < n; ++s) M = fmaxf(M, ml[s * mstride]);
     float Lsum = 0.f;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    const float* po = p.part_o + (bbase + g) * D + d4 * 4;
+    const int64_t ostride = (int64_t)p.hq * D;
+#pragma unroll 4
     for (int s = 0; s < n; ++s) {
-      const float* ml = p.part_ml + (base + (int64_t)s * p.hq + h) * 2;
-      const float f = __builtin_amdgcn_exp2f(ml[0] - M);
-      w[h * kMaxSplits + s] = f;
-      Lsum += ml[1] * f;
+      const float f = __builtin_amdgcn_exp2f(ml[s * mstride] - M);
+      Lsum += f * ml[s * mstride + 1];
+      a += f * *reinterpret_cast<const f32x4*>(po + s * ostride);
     }
     const float inv = 1.f / Lsum;
-    for (int s = 0; s < n; ++s) w[h * kMaxSplits + s] *= inv;
-  }
-  __syncthreads();
-  constexpr int C = D / 4;  // float4 chunks per head row
-  T* o = reinterpret_cast<T*>(p.out) + (int64_t)b * p.hq * D;
-  for (int i = threadIdx.x; i < p.hq * C; i += blockDim.x) {
-    const int h = i / C, c = i % C;
-    f32x4 a = {0.f, 0.f, 0.f, 0.f};
-    for (int s = 0; s < n; ++s) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(p.part_o + (base + (int64_t)s * p.hq + h) * D + c * 4);
-      a += w[h * kMaxSplits + s] * x;
-    }
+    T tmp[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) o[h * D + c * 4 + e] = from_f32<T>(a[e]);
+    for (int e = 0; e < 4; ++e) tmp[e] = from_f32<T>(a[e] * inv);
+    T* dst = o + g * D + d4 * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = tmp[e];
   }
 }
 
+// Wavefronts per workgroup (kv heads handled by one workgroup). Small
+// workgroups let a CU start new work as soon as any wave finishes.
+#ifndef MSGL_DECODE_WAVES_PER_WG
+#define MSGL_DECODE_WAVES_PER_WG 4
+#endif
+
 template <typename T, int D, int G>
 static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
-  const int nwaves = p.hkv < 8 ? p.hkv : 8;
-  const size_t lds = (size_t)nwaves * kLdsPerWave * sizeof(float);
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, G>), dim3(p.max_splits, batch), dim3(64 * nwaves), lds, stream, p);
+  const int nwaves = p.hkv < MSGL_DECODE_WAVES_PER_WG ? p.hkv : MSGL_DECODE_WAVES_PER_WG;
+  const int ngrp = (p.hkv + nwaves - 1) / nwaves;
+  const size_t lds = ((size_t)kSeg + kSlotPad + (size_t)nwaves * (kLdsPerWave + 16 * k_lds_stride<T, D>() / 4)) *
+                     sizeof(float);
+  hipLaunchKernelGGL((paged_decode_kernel<T, D, G>), dim3(p.max_splits * ngrp, batch), dim3(64 * nwaves), lds, stream,
+                     p);
   MSGL_CHECK_LAUNCH("msgl_paged_decode");
   if (p.max_splits > 1) {
-    hipLaunchKernelGGL((paged_decode_merge_kernel<T, D>), dim3(batch), dim3(256), 0, stream, p);
+    const int units = batch * p.hkv;
+    hipLaunchKernelGGL((paged_decode_merge_kernel<T, D, G>), dim3((units + 3) / 4), dim3(256), 0, stream, p, batch);
     MSGL_CHECK_LAUNCH("msgl_paged_decode (merge)");
   }
   return MSGL_OK;
@@ -387,6 +474,9 @@ static int dispatch_dim(const DecodeParams& p, int batch, int head_dim, int grou
   }
 }
 
+// Workspace layout: [m,l B*S*Hq*2 f32 | acc B*S*Hq*D f32], each region 256-byte aligned.
+static inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
 }  // namespace msgl
 
 extern "C" int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
@@ -404,14 +494,14 @@ extern "C" int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_k
   return (int32_t)s;
 }
 
-extern "C" int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, int32_t head_dim,
-                                                    int32_t max_splits) {
-  if (batch <= 0 || num_qo_heads <= 0 || head_dim <= 0) return 0;
+extern "C" int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                                    int32_t head_dim, int32_t max_splits) {
+  using msgl::align256;
+  if (batch <= 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
+  if (max_splits > msgl::kMaxSplits) max_splits = msgl::kMaxSplits;
   if (max_splits <= 1) return 0;
   const int64_t units = (int64_t)batch * max_splits * num_qo_heads;
-  const int64_t o_bytes = units * head_dim * 4;
-  const int64_t ml_bytes = units * 2 * 4;
-  return ((o_bytes + 255) / 256) * 256 + ml_bytes;
+  return align256(units * 2 * 4) + align256(units * head_dim * 4);
 }
 
 extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* v_pool, const int32_t* kv_indptr,
@@ -426,7 +516,6 @@ extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* 
   MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "msgl_paged_decode: sizes must be > 0");
   MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "msgl_paged_decode: Hq (%d) must be a multiple of Hkv (%d)",
                  num_qo_heads, num_kv_heads);
-  MSGL_CHECK_ARG(num_qo_heads <= 64, "msgl_paged_decode: Hq must be <= 64 (got %d)", num_qo_heads);
   MSGL_CHECK_ARG(page_size >= 1, "msgl_paged_decode: page_size must be >= 1");
   MSGL_CHECK_ARG(page_size == 1 || seq_lens != nullptr, "msgl_paged_decode: page_size > 1 needs seq_lens");
   MSGL_CHECK_ARG(num_slots > 0 && num_slots <= ((int64_t)1 << 31) - 1,
@@ -440,9 +529,10 @@ extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* 
   }
   if (max_splits <= 0) max_splits = msgl_paged_decode_default_splits(batch, num_kv_heads, 0);
   if (max_splits > kMaxSplits) max_splits = kMaxSplits;
-  const int64_t need = msgl_paged_decode_workspace_size(batch, num_qo_heads, head_dim, max_splits);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
-    set_error("msgl_paged_decode: workspace of %lld bytes needed, %lld given", (long long)need,
+  const int64_t need =
+      msgl_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)) {
+    set_error("msgl_paged_decode: 256-byte aligned workspace of %lld bytes needed, %lld given", (long long)need,
               (long long)workspace_bytes);
     return MSGL_ERR_WORKSPACE;
   }
@@ -455,10 +545,9 @@ extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* 
   p.seq_lens = seq_lens;
   p.out = out;
   const int64_t units = (int64_t)batch * max_splits * num_qo_heads;
-  p.part_o = reinterpret_cast<float*>(workspace);
-  p.part_ml = need > 0 ? reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) +
-                                                  ((units * head_dim * 4 + 255) / 256) * 256)
-                       : nullptr;
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  p.part_ml = need > 0 ? reinterpret_cast<float*>(ws) : nullptr;
+  p.part_o = need > 0 ? reinterpret_cast<float*>(ws + align256(units * 2 * 4)) : nullptr;
   p.num_slots = num_slots;
   p.hq = num_qo_heads;
   p.hkv = num_kv_heads;

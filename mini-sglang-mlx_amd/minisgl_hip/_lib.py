@@ -42,7 +42,7 @@ SIGNATURES = {
         [_c_p, _c_p, _c_p, _c_p, _c_p, _c_i64, _c_i32, _c_i32, _c_i64, _c_i32, _c_p],
     ),
     "msgl_paged_decode_default_splits": (_c_i32, [_c_i32, _c_i32, _c_i32]),
-    "msgl_paged_decode_workspace_size": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
+    "msgl_paged_decode_workspace_size": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "msgl_paged_decode": (
         ctypes.c_int,
         [

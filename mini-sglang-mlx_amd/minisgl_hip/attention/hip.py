@@ -3,7 +3,7 @@
 Decode metadata is the CSR form of attention/metal.py:145-152
 (kv_indptr [B+1], kv_indices [sum L] token slots), built with numpy from the
 host page table and copied to the device once per step; every layer then
-runs one paged-decode launch (+ the split-K merge) over its own pool.
+runs one paged-decode launch (plus the split-K merge) over its own pool.
 Prefill metadata mirrors attention/base.py:70-83 and additionally carries the
 packed ragged description (q_indptr, kv_indptr, kv_indices, seq_lens) that
 the ragged prefill kernel reads in one launch instead of a per-request loop.
@@ -78,11 +78,12 @@ class HipAttnBackend(BaseAttnBackend):
         )
 
     def _decode_workspace(self, batch_size: int, max_splits: int) -> Optional[torch.Tensor]:
-        need = ops.decode_workspace_bytes(batch_size, self.config.num_qo_heads, self.config.head_dim, max_splits)
+        cfg = self.config
+        need = ops.decode_workspace_bytes(batch_size, cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, max_splits)
         if need == 0:
             return None
         if self._workspace is None or self._workspace.numel() < need:
-            # one buffer reused by every layer: layers run in stream order
+            # one buffer reused by every layer and step: launches run in stream order
             self._workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
         return self._workspace
 

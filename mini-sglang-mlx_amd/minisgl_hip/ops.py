@@ -59,8 +59,22 @@ def default_splits(batch: int, num_kv_heads: int, max_seq_len: int = 0) -> int:
     return int(_lib.load().msgl_paged_decode_default_splits(batch, num_kv_heads, max_seq_len))
 
 
-def decode_workspace_bytes(batch: int, num_qo_heads: int, head_dim: int, max_splits: int) -> int:
-    return int(_lib.load().msgl_paged_decode_workspace_size(batch, num_qo_heads, head_dim, max_splits))
+def decode_workspace_bytes(batch: int, num_qo_heads: int, num_kv_heads: int, head_dim: int, max_splits: int) -> int:
+    return int(
+        _lib.load().msgl_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, max_splits)
+    )
+
+
+def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, head_dim: int, max_splits: int,
+                     device) -> Optional[torch.Tensor]:
+    """A workspace for ``paged_decode_attention`` (None when no split-K).
+
+    Consecutive calls on one stream may reuse it; overlapping calls may not.
+    """
+    need = decode_workspace_bytes(batch, num_qo_heads, num_kv_heads, head_dim, max_splits)
+    if need == 0:
+        return None
+    return torch.empty(need, dtype=torch.uint8, device=device)
 
 
 def paged_decode_attention(
@@ -82,7 +96,8 @@ def paged_decode_attention(
 
     q [B, Hq, D]; pools [N, Hkv, D]; kv_indptr [B+1] int32; kv_indices int32
     (token slots, or page ids when page_size > 1 with seq_lens [B] given).
-    Returns o [B, Hq, D] in q's dtype.
+    Returns o [B, Hq, D] in q's dtype. ``workspace`` (from ``decode_workspace``)
+    is allocated per call when not given.
     """
     if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
         raise ValueError("q must be [B, Hq, D] and pools [N, Hkv, D]")
@@ -112,7 +127,7 @@ def paged_decode_attention(
     lib = _lib.load()
     if max_splits is None:
         max_splits = int(lib.msgl_paged_decode_default_splits(b, hkv, max_seq_len))
-    need = int(lib.msgl_paged_decode_workspace_size(b, hq, d, max_splits))
+    need = int(lib.msgl_paged_decode_workspace_size(b, hq, hkv, d, max_splits))
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     status = lib.msgl_paged_decode(

@@ -36,10 +36,13 @@ def test_every_declared_symbol_is_exported_and_bound():
 def test_abi_version_and_sizes():
     lib = _lib.load()
     assert lib.msgl_abi_version() == 1
-    assert lib.msgl_paged_decode_workspace_size(128, 16, 128, 1) == 0
-    ws = lib.msgl_paged_decode_workspace_size(128, 16, 128, 16)
+    assert lib.msgl_paged_decode_workspace_size(128, 16, 8, 128, 1) == 0
+    ws = lib.msgl_paged_decode_workspace_size(128, 16, 8, 128, 16)
     units = 128 * 16 * 16
-    assert ws == ((units * 128 * 4 + 255) // 256) * 256 + units * 8
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert ws == up(units * 8) + up(units * 128 * 4)
+    assert lib.msgl_paged_decode_workspace_size(1, 16, 8, 128, 1000) == lib.msgl_paged_decode_workspace_size(
+        1, 16, 8, 128, 64)
     assert 1 <= lib.msgl_paged_decode_default_splits(128, 8, 2048) <= 64
     assert lib.msgl_paged_decode_default_splits(1, 8, 32768) == 64
     assert lib.msgl_paged_decode_default_splits(1, 8, 100) == 2  # capped by ceil(100 / 64)
