@@ -8,8 +8,10 @@ decode attention runs over the pool. Inputs are resident in HBM before timing.
 
 Prints one JSON line. ``value`` is algorithmic GB/s over the whole step
 (decode bytes = ΣL·Hkv·D·2·2 + B·Hq·D·2·2 + ΣL·4 + (B+1)·4 per layer, plus the
-KV store's read+write); ``roofline`` is the decode launch alone (HIP events
-around every decode call inside the timed region, on the launch stream);
+KV store's read+write); ``roofline`` is one layer's attention op alone -- the
+paged-decode kernel with the KV store fused in, plus its split-K merge kernel
+-- timed with HIP events around one layer per step (rotating through the
+layers) inside the timed region, on the launch stream;
 ``cpu_baseline`` times the CPU restatement of the reference's naive backend.
 """
 
@@ -134,34 +136,37 @@ def main():
     ws = ops.decode_workspace(BATCH, HQ, HKV, D, splits, dev)
     scale = D**-0.5
 
-    def step(events=None):
+    def step(timed_layer=-1, events=None):
+        # per layer: the KV store of the new token fused into the paged-decode
+        # launch (msgl_paged_decode_store), then the split-K merge. One layer per
+        # step is bracketed by HIP events (an event record costs a queue
+        # barrier, so recording around every layer would slow the step down).
         for layer in range(LAYERS):
-            ops.store_kv(ks[layer], vs[layer], out_loc, kps[layer], vps[layer])
-            if events is not None:
-                events[layer][0].record()
+            if layer == timed_layer:
+                events[0].record()
             ops.paged_decode_attention(qs[layer], kps[layer], vps[layer], indptr, indices, scale,
-                                       max_splits=splits, out=outs[layer], workspace=ws)
-            if events is not None:
-                events[layer][1].record()
+                                       max_splits=splits, out=outs[layer], workspace=ws,
+                                       new_kv=(ks[layer], vs[layer], out_loc))
+            if layer == timed_layer:
+                events[1].record()
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    ev = [[[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in range(LAYERS)]
-          for _ in range(args.steps)]
+    ev = [[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in range(args.steps)]
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
-        step(ev[s])
+        step(s % LAYERS, ev[s])
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
-    dec_ms = [e0.elapsed_time(e1) for st in ev for (e0, e1) in st]
+    dec_ms = [e0.elapsed_time(e1) for (e0, e1) in ev]
     dec_avg_s = float(np.mean(dec_ms)) / 1e3
     ms_per_step = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9
-    achieved = dec_bytes / dec_avg_s / 1e9
+    achieved = (dec_bytes + store_bytes) / dec_avg_s / 1e9  # one layer's decode+store launch + merge
     traffic = read_traffic()
 
     cpu = None
@@ -201,7 +206,7 @@ def main():
             "workload": (
                 "paged decode, Qwen3-0.6B attention (16 q / 8 kv heads, head_dim 128), 28 layers; batch 128, "
                 "context U[200,2048] (seed 0), page_size 1, 262144-slot bf16 pool per layer, random slots; "
-                "per layer: KV-store scatter of the new token + paged decode"
+                "per layer: KV store of the new token + paged decode (one fused launch) + split-K merge"
             ),
             "batch": BATCH,
             "sum_context": int(c.lens.sum()),

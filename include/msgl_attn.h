@@ -13,6 +13,7 @@
  *   msgl_store_kv            kvcache/pool.py:47-50        MHAKVCache.store_kv
  *   msgl_paged_decode        attention/metal.py:112-131   paged_decode_attention
  *                            (semantics of attention/naive.py:50-60 forward_decode)
+ *   msgl_paged_decode_store  kvcache/pool.py:47-50 + attention/metal.py:112-131 in one launch
  *   msgl_prefill_ragged      attention/base.py:85-105     BaseAttnBackend._forward_prefill
  *
  * Layouts (identical to the reference, no transposes at the boundary):
@@ -99,6 +100,24 @@ int msgl_paged_decode(const void* q, const void* k_pool, const void* v_pool, con
                       int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                       int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                       void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * KV store fused into paged decode: msgl_store_kv(k_new, v_new, out_loc, ...)
+ * followed by msgl_paged_decode(...), in one decode launch (+ the split-K
+ * merge). Replaces the per-layer pair kvcache/pool.py:47-50 +
+ * attention/metal.py:112-131 as called at layers.py:109-110.
+ *   k_new, v_new  [B, Hkv, D] this step's rows, one new token per request
+ *   out_loc       [B] slot of each request's newest token; it must be the slot
+ *                 of position L_b - 1 (always the case in decode: the new
+ *                 token is the last position, scheduler/scheduler.py:154-157)
+ * The pools are written only at out_loc (entries outside [0, num_slots) are
+ * skipped). Output and pool contents equal the two-call sequence bit for bit.
+ */
+int msgl_paged_decode_store(const void* q, const void* k_new, const void* v_new, const int32_t* out_loc,
+                            void* k_pool, void* v_pool, const int32_t* kv_indptr, const int32_t* kv_indices,
+                            const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                            int32_t head_dim, int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                            int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Ragged chunked-prefill attention over a paged pool, one launch per batch.

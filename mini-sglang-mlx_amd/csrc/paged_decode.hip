@@ -14,9 +14,11 @@
 //    16 tokens (>= kMinChunk), decided on the device from L_b alone. A
 //    single-chunk request writes its final row. Otherwise every chunk writes
 //    fp32 partials (acc, m, l) and a merge kernel with one wavefront per
-//    (request, kv head) combines them. (Merging inside the decode launch
-//    needs a device-scope release per chunk, which on this part writes back
-//    the XCD's L2 each time and costs far more than a second launch.)
+//    (request, kv head) combines them. Merging inside the decode launch was
+//    measured slower on MI355X: a device-scope fence per chunk writes back and
+//    invalidates the XCD's L2, and even fence-free agent-coherent partials
+//    leave every chunk waiting on write-through stores and an atomic round
+//    trip before its slot frees -- more than the second launch costs.
 //  * Q.K^T runs on the matrix cores: v_mfma_f32_16x16x32_{bf16,f16} (or
 //    16x16x4 f32), A = the G query heads of the kv head (rows >= G are zero),
 //    B = 16 K rows (no conversion). Output: lane (t = l%16, row group l/16)
@@ -41,7 +43,10 @@
 
 namespace msgl {
 
-constexpr int kMinChunk = 64;   // smallest split-K chunk (tokens)
+#ifndef MSGL_DECODE_MIN_CHUNK
+#define MSGL_DECODE_MIN_CHUNK 64
+#endif
+constexpr int kMinChunk = MSGL_DECODE_MIN_CHUNK;  // smallest split-K chunk (tokens)
 constexpr int kMaxSplits = 64;  // bound on splits per request
 constexpr int kSeg = 512;       // token slots staged in LDS at a time
 constexpr int kSlotPad = 16 * 7;  // room for up to 7 padding tiles of prefetch
@@ -115,6 +120,12 @@ struct DecodeParams {
   void* out;
   float* part_ml;     // [B, S, Hq, 2]
   float* part_o;      // [B, S, Hq, D]
+  // fused KV store (all null for plain decode): this step's rows [B, Hkv, D]
+  const void* k_new;
+  const void* v_new;
+  const int32_t* out_loc;  // [B] slot of each request's newest token (position L_b - 1)
+  void* k_pool_w;
+  void* v_pool_w;
   int64_t num_slots;
   int hq, hkv, page_size, max_splits;
   float scale_log2;
@@ -233,6 +244,23 @@ void paged_decode_kernel(DecodeParams p) {
     const uint8_t* kbase_p = reinterpret_cast<const uint8_t*>(p.k_pool) + (int64_t)kvh_c * D * ES + vc * VEC * ES;
     const uint8_t* vbase_p = reinterpret_cast<const uint8_t*>(p.v_pool) + (int64_t)kvh_c * D * ES + vc * VEC * ES;
 
+    // Fused KV store: the chunk holding position L-1 (the new token) writes its
+    // rows to the pool and reads them from k_new/v_new instead -- no other
+    // unit reads that slot, so the write needs no ordering inside the launch.
+    const bool fused = p.k_new != nullptr;
+    const int new_pos = fused && t1 == L ? L - 1 : 0x7fffffff;  // absolute position, or never
+    const int64_t new_off = ((int64_t)b * p.hkv + kvh_c) * D * ES + vc * VEC * ES;
+    const uint8_t* knew_p = fused ? reinterpret_cast<const uint8_t*>(p.k_new) + new_off : nullptr;
+    const uint8_t* vnew_p = fused ? reinterpret_cast<const uint8_t*>(p.v_new) + new_off : nullptr;
+    if (active && new_pos != 0x7fffffff && lane < LPR) {
+      const int64_t slot = p.out_loc[b];
+      if (slot >= 0 && slot < p.num_slots) {
+        const int64_t dst = slot * row_stride + (int64_t)kvh * D * ES + vc * VEC * ES;
+        st16(reinterpret_cast<uint8_t*>(p.k_pool_w) + dst, ld16(knew_p));
+        st16(reinterpret_cast<uint8_t*>(p.v_pool_w) + dst, ld16(vnew_p));
+      }
+    }
+
     for (int s0 = t0; s0 < t1; s0 += kSeg) {
       const int seg_len = min(kSeg, t1 - s0);
       const int ntile = (seg_len + 15) >> 4;
@@ -254,9 +282,11 @@ void paged_decode_kernel(DecodeParams p) {
         const int base = tile * 16;
 #pragma unroll
         for (int i = 0; i < NLV; ++i) {
-          const int64_t off = (int64_t)slots_lds[base + vr + R * i] * row_stride;
-          buf.k[i] = ld16_stream(kbase_p + off);
-          buf.v[i] = ld16_stream(vbase_p + off);
+          const int pos = base + vr + R * i;
+          const int64_t off = (int64_t)slots_lds[pos] * row_stride;
+          const bool is_new = s0 + pos >= new_pos;  // the new token and the padding that repeats it
+          buf.k[i] = ld16_stream(is_new ? knew_p : kbase_p + off);
+          buf.v[i] = ld16_stream(is_new ? vnew_p : vbase_p + off);
         }
       };
 
@@ -384,8 +414,8 @@ void paged_decode_kernel(DecodeParams p) {
 // Merge split-K partials, one wavefront per (request, kv head):
 //   o = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
 // (the combine of the Metal kernel's simdgroup merge, attention/metal.py:75-94).
-// Lanes own float4 chunks of the G*D outputs; every split's loads are
-// independent, so a wavefront keeps all of them in flight.
+// Lanes own float4 chunks of the G*D outputs; the partials of up to 8 splits
+// are loaded in one batch (one memory round trip) and combined online.
 template <typename T, int D, int G>
 __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p, int batch) {
   const int unit = blockIdx.x * (blockDim.x >> 6) + (threadIdx.x >> 6);  // (b, kvh)
@@ -398,22 +428,42 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p,
   if (n <= 1) return;
   const int64_t bbase = (int64_t)b * p.max_splits * p.hq + kvh * G;
   constexpr int C4 = D / 4;
+  constexpr int NB = 8;  // splits whose partials are loaded in one batch
   T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D;
   for (int c = lane; c < G * C4; c += 64) {
     const int g = c / C4, d4 = c % C4;
-    const float* ml = p.part_ml + (bbase + g) * 2;
-    const int64_t mstride = (int64_t)p.hq * 2;
-    float M = -INFINITY;
-    for (int s = 0; s < n; ++s) M = fmaxf(M, ml[s * mstride]);
-    float Lsum = 0.f;
-    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    const float2* ml = reinterpret_cast<const float2*>(p.part_ml) + bbase + g;
     const float* po = p.part_o + (bbase + g) * D + d4 * 4;
+    const int64_t mstride = p.hq;  // float2 units
     const int64_t ostride = (int64_t)p.hq * D;
-#pragma unroll 4
-    for (int s = 0; s < n; ++s) {
-      const float f = __builtin_amdgcn_exp2f(ml[s * mstride] - M);
-      Lsum += f * ml[s * mstride + 1];
-      a += f * *reinterpret_cast<const f32x4*>(po + s * ostride);
+    float M = -INFINITY, Lsum = 0.f;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < n; s0 += NB) {
+      // issue every load of this batch before using any of them
+      float2 mlv[NB];
+      f32x4 xv[NB];
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int sp = min(s0 + i, n - 1);
+        mlv[i] = ml[sp * mstride];
+        xv[i] = *reinterpret_cast<const f32x4*>(po + sp * ostride);
+      }
+      float Mb = M;
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+        if (s0 + i < n) Mb = fmaxf(Mb, mlv[i].x);
+      const float r = __builtin_amdgcn_exp2f(M - Mb);  // rescale what was combined so far
+      Lsum *= r;
+      a *= r;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        if (s0 + i < n) {
+          const float f = __builtin_amdgcn_exp2f(mlv[i].x - Mb);
+          Lsum += f * mlv[i].y;
+          a += f * xv[i];
+        }
+      }
+      M = Mb;
     }
     const float inv = 1.f / Lsum;
     T tmp[4];
@@ -424,12 +474,6 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p,
     for (int e = 0; e < 4; ++e) dst[e] = tmp[e];
   }
 }
-
-// Wavefronts per workgroup (kv heads handled by one workgroup). Small
-// workgroups let a CU start new work as soon as any wave finishes.
-#ifndef MSGL_DECODE_WAVES_PER_WG
-#define MSGL_DECODE_WAVES_PER_WG 4
-#endif
 
 template <typename T, int D, int G>
 static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
@@ -480,10 +524,11 @@ static inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 }  // namespace msgl
 
 extern "C" int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
-  // Aim for ~16k wavefronts (about 4 rounds of a full MI355X at 4 waves/SIMD)
-  // so ragged lengths balance, without chunks shorter than kMinChunk.
+  // Aim for ~4096 wavefronts (a bit over one round of MI355X at 3 waves/SIMD):
+  // enough units for ragged lengths to balance, few enough that the split-K
+  // partials and the merge stay small. No chunk is shorter than kMinChunk.
   if (batch <= 0 || num_kv_heads <= 0) return 1;
-  const int64_t target_waves = 16384;
+  const int64_t target_waves = 4096;
   int64_t s = (target_waves + (int64_t)batch * num_kv_heads - 1) / ((int64_t)batch * num_kv_heads);
   if (max_seq_len > 0) {
     const int64_t cap = (max_seq_len + msgl::kMinChunk - 1) / msgl::kMinChunk;
@@ -504,27 +549,62 @@ extern "C" int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_q
   return align256(units * 2 * 4) + align256(units * head_dim * 4);
 }
 
+static int paged_decode_impl(const char* fn, const void* q, const void* k_new, const void* v_new,
+                             const int32_t* out_loc, const void* k_pool, const void* v_pool,
+                             const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                             int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                             void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
 extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* v_pool, const int32_t* kv_indptr,
                                  const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
                                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                  int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                                  void* workspace, int64_t workspace_bytes, void* stream) {
+  return paged_decode_impl("msgl_paged_decode", q, nullptr, nullptr, nullptr, k_pool, v_pool, kv_indptr, kv_indices,
+                           seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size, num_slots, dtype, scale,
+                           max_splits, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int msgl_paged_decode_store(const void* q, const void* k_new, const void* v_new, const int32_t* out_loc,
+                                       void* k_pool, void* v_pool, const int32_t* kv_indptr,
+                                       const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                                       int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                       int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                                       int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
   using namespace msgl;
   clear_error();
-  MSGL_CHECK_ARG(batch >= 0 && batch <= 65535, "msgl_paged_decode: batch must be in [0, 65535]");
+  MSGL_CHECK_ARG(k_new && v_new && out_loc, "msgl_paged_decode_store: null k_new, v_new or out_loc");
+  MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
+                 "msgl_paged_decode_store: k_new and v_new must be 16-byte aligned");
+  return paged_decode_impl("msgl_paged_decode_store", q, k_new, v_new, out_loc, k_pool, v_pool, kv_indptr,
+                           kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size, num_slots,
+                           dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
+}
+
+static int paged_decode_impl(const char* fn, const void* q, const void* k_new, const void* v_new,
+                             const int32_t* out_loc, const void* k_pool, const void* v_pool,
+                             const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                             int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                             void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(batch >= 0 && batch <= 65535, "%s: batch must be in [0, 65535]", fn);
   if (batch == 0) return MSGL_OK;
-  MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "msgl_paged_decode: sizes must be > 0");
-  MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "msgl_paged_decode: Hq (%d) must be a multiple of Hkv (%d)",
-                 num_qo_heads, num_kv_heads);
-  MSGL_CHECK_ARG(page_size >= 1, "msgl_paged_decode: page_size must be >= 1");
-  MSGL_CHECK_ARG(page_size == 1 || seq_lens != nullptr, "msgl_paged_decode: page_size > 1 needs seq_lens");
+  MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "%s: sizes must be > 0", fn);
+  MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "%s: Hq (%d) must be a multiple of Hkv (%d)",
+                 fn, num_qo_heads, num_kv_heads);
+  MSGL_CHECK_ARG(page_size >= 1, "%s: page_size must be >= 1", fn);
+  MSGL_CHECK_ARG(page_size == 1 || seq_lens != nullptr, "%s: page_size > 1 needs seq_lens", fn);
   MSGL_CHECK_ARG(num_slots > 0 && num_slots <= ((int64_t)1 << 31) - 1,
-                 "msgl_paged_decode: num_slots must be in [1, 2^31)");
-  MSGL_CHECK_ARG(q && k_pool && v_pool && kv_indptr && kv_indices && out, "msgl_paged_decode: null pointer");
+                 "%s: num_slots must be in [1, 2^31)", fn);
+  MSGL_CHECK_ARG(q && k_pool && v_pool && kv_indptr && kv_indices && out, "%s: null pointer", fn);
   MSGL_CHECK_ARG(((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) % 16 == 0,
-                 "msgl_paged_decode: q, pools and out must be 16-byte aligned");
+                 "%s: q, pools and out must be 16-byte aligned", fn);
   if (dtype_size(dtype) == 0) {
-    set_error("msgl_paged_decode: unknown dtype %d", dtype);
+    set_error("%s: unknown dtype %d", fn, dtype);
     return MSGL_ERR_UNSUPPORTED;
   }
   if (max_splits <= 0) max_splits = msgl_paged_decode_default_splits(batch, num_kv_heads, 0);
@@ -532,7 +612,7 @@ extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* 
   const int64_t need =
       msgl_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)) {
-    set_error("msgl_paged_decode: 256-byte aligned workspace of %lld bytes needed, %lld given", (long long)need,
+    set_error("%s: 256-byte aligned workspace of %lld bytes needed, %lld given", fn, (long long)need,
               (long long)workspace_bytes);
     return MSGL_ERR_WORKSPACE;
   }
@@ -544,6 +624,11 @@ extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* 
   p.kv_indices = kv_indices;
   p.seq_lens = seq_lens;
   p.out = out;
+  p.k_new = k_new;
+  p.v_new = v_new;
+  p.out_loc = out_loc;
+  p.k_pool_w = const_cast<void*>(k_pool);
+  p.v_pool_w = const_cast<void*>(v_pool);
   const int64_t units = (int64_t)batch * max_splits * num_qo_heads;
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   p.part_ml = need > 0 ? reinterpret_cast<float*>(ws) : nullptr;

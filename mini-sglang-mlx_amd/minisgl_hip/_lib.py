@@ -53,6 +53,17 @@ SIGNATURES = {
             _c_i32, _c_p, _c_p, _c_i64, _c_p,  # max_splits, out, workspace, ws_bytes, stream
         ],
     ),
+    "msgl_paged_decode_store": (
+        ctypes.c_int,
+        [
+            _c_p, _c_p, _c_p, _c_p,  # q, k_new, v_new, out_loc
+            _c_p, _c_p,  # k_pool, v_pool
+            _c_p, _c_p, _c_p,  # kv_indptr, kv_indices, seq_lens
+            _c_i32, _c_i32, _c_i32, _c_i32,  # batch, Hq, Hkv, D
+            _c_i32, _c_i64, _c_i32, _c_f,  # page_size, num_slots, dtype, scale
+            _c_i32, _c_p, _c_p, _c_i64, _c_p,  # max_splits, out, workspace, ws_bytes, stream
+        ],
+    ),
     "msgl_prefill_ragged": (
         ctypes.c_int,
         [

@@ -3,7 +3,8 @@
 Decode metadata is the CSR form of attention/metal.py:145-152
 (kv_indptr [B+1], kv_indices [sum L] token slots), built with numpy from the
 host page table and copied to the device once per step; every layer then
-runs one paged-decode launch (plus the split-K merge) over its own pool.
+runs one paged-decode launch (plus the split-K merge) over its own pool, with
+the step's KV store performed inside the decode launch.
 Prefill metadata mirrors attention/base.py:70-83 and additionally carries the
 packed ragged description (q_indptr, kv_indptr, kv_indices, seq_lens) that
 the ragged prefill kernel reads in one launch instead of a per-request loop.
@@ -54,10 +55,21 @@ class HipPrefillDevice:
 
 
 class HipAttnBackend(BaseAttnBackend):
-    def __init__(self, config, kv_cache, page_table: np.ndarray) -> None:
+    """``fuse_decode_store``: during decode steps the pool defers ``store_kv`` and
+    ``forward_decode`` performs it inside the decode launch (one kernel instead of
+    two per layer); results and pool contents are identical to the eager order."""
+
+    def __init__(self, config, kv_cache, page_table: np.ndarray, fuse_decode_store: bool = True) -> None:
         super().__init__(config, kv_cache, page_table)
-        self.device = kv_cache.k_cache(0).device
+        self.device = kv_cache.k[0].device
+        self.fuse_decode_store = fuse_decode_store and hasattr(kv_cache, "take_pending")
         self._workspace: Optional[torch.Tensor] = None
+
+    def prepare_metadata(self, batch: "Batch") -> None:
+        if self.fuse_decode_store:
+            self.kv_cache.flush()
+            self.kv_cache.defer_stores = batch.is_decode
+        super().prepare_metadata(batch)
 
     # ------------------------------------------------------------------ decode
 
@@ -89,15 +101,21 @@ class HipAttnBackend(BaseAttnBackend):
 
     def forward_decode(self, q: torch.Tensor, layer_id: int, meta: HipDecodeMetadata) -> torch.Tensor:
         ws = self._decode_workspace(q.shape[0], meta.max_splits)
+        pending = self.kv_cache.take_pending(layer_id) if self.fuse_decode_store else None
+        if pending is not None and pending[0].shape[0] != q.shape[0]:
+            k, v, out_loc = pending  # not one new token per request: store eagerly
+            ops.store_kv(k, v, out_loc, self.kv_cache.k[layer_id], self.kv_cache.v[layer_id])
+            pending = None
         return ops.paged_decode_attention(
             q,
-            self.kv_cache.k_cache(layer_id),
-            self.kv_cache.v_cache(layer_id),
+            self.kv_cache.k[layer_id] if pending is not None else self.kv_cache.k_cache(layer_id),
+            self.kv_cache.v[layer_id] if pending is not None else self.kv_cache.v_cache(layer_id),
             meta.kv_indptr,
             meta.kv_indices,
             self.scale,
             max_splits=meta.max_splits,
             workspace=ws,
+            new_kv=pending,
         )
 
     # ------------------------------------------------------------------ prefill

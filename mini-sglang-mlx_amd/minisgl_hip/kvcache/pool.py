@@ -6,15 +6,23 @@
 A slot is an index along dim 0. One K and one V buffer per layer, zero
 initialised, in the model dtype (kvcache/pool.py:25-39). ``store_kv`` writes
 this step's rows with the HIP scatter kernel, in place.
+
+Deferred stores: with ``defer_stores`` set (the hip backend sets it for decode
+steps), ``store_kv`` only records the rows; the backend then performs the
+store inside its decode launch (``take_pending``). Any other read of that
+layer's pool (``k_cache``/``v_cache``) first performs the recorded store, so
+every reader still observes the pool exactly as after an eager store.
 """
 
 from __future__ import annotations
 
-from typing import List
+from typing import List, Optional, Tuple
 
 import torch
 
 from .. import ops
+
+PendingStore = Tuple[torch.Tensor, torch.Tensor, torch.Tensor]  # (k, v, out_loc)
 
 
 class MHAKVCache:
@@ -35,16 +43,38 @@ class MHAKVCache:
         self.num_kv_heads = num_kv_heads
         self.head_dim = head_dim
         self.dtype = dtype
+        self.defer_stores = False
+        self._pending: List[Optional[PendingStore]] = [None] * num_layers
 
     def k_cache(self, layer_id: int) -> torch.Tensor:
+        self.flush(layer_id)
         return self.k[layer_id]
 
     def v_cache(self, layer_id: int) -> torch.Tensor:
+        self.flush(layer_id)
         return self.v[layer_id]
 
     def store_kv(self, k: torch.Tensor, v: torch.Tensor, out_loc: torch.Tensor, layer_id: int) -> None:
         """kvcache/pool.py:47-50: write this step's k/v ([T, Hkv, D]) to slots out_loc ([T])."""
-        ops.store_kv(k, v, out_loc, self.k[layer_id], self.v[layer_id])
+        if self.defer_stores:
+            self.flush(layer_id)
+            self._pending[layer_id] = (k, v, out_loc)
+        else:
+            ops.store_kv(k, v, out_loc, self.k[layer_id], self.v[layer_id])
+
+    def take_pending(self, layer_id: int) -> Optional[PendingStore]:
+        """Hand a recorded store to the caller, who becomes responsible for performing it."""
+        pending, self._pending[layer_id] = self._pending[layer_id], None
+        return pending
+
+    def flush(self, layer_id: Optional[int] = None) -> None:
+        """Perform recorded stores (of one layer, or of all layers)."""
+        layers = range(self.num_layers) if layer_id is None else (layer_id,)
+        for i in layers:
+            pending = self.take_pending(i)
+            if pending is not None:
+                k, v, out_loc = pending
+                ops.store_kv(k, v, out_loc, self.k[i], self.v[i])
 
     @property
     def nbytes(self) -> int:

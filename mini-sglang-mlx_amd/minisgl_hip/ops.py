@@ -91,13 +91,17 @@ def paged_decode_attention(
     max_seq_len: int = 0,
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
+    new_kv: Optional[tuple] = None,
 ) -> torch.Tensor:
     """Paged decode attention; counterpart of attention/metal.py:112-131.
 
     q [B, Hq, D]; pools [N, Hkv, D]; kv_indptr [B+1] int32; kv_indices int32
     (token slots, or page ids when page_size > 1 with seq_lens [B] given).
     Returns o [B, Hq, D] in q's dtype. ``workspace`` (from ``decode_workspace``)
-    is allocated per call when not given.
+    is allocated per call when not given. With ``new_kv = (k_new, v_new,
+    out_loc)`` the KV store of this step's rows (kvcache/pool.py:47-50) runs in
+    the same launch: k_pool[out_loc] = k_new, v_pool[out_loc] = v_new, where
+    out_loc[b] is the slot of request b's last position.
     """
     if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
         raise ValueError("q must be [B, Hq, D] and pools [N, Hkv, D]")
@@ -130,15 +134,29 @@ def paged_decode_attention(
     need = int(lib.msgl_paged_decode_workspace_size(b, hq, hkv, d, max_splits))
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
-    status = lib.msgl_paged_decode(
-        _lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool),
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
+    common = (
         _lib.ptr(kv_indptr), _lib.ptr(kv_indices), _lib.ptr(seq_lens),
         b, hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
-        max_splits, _lib.ptr(out), _lib.ptr(workspace),
-        0 if workspace is None else workspace.numel() * workspace.element_size(),
-        _lib.current_stream(dev),
+        max_splits, _lib.ptr(out), _lib.ptr(workspace), ws_bytes, _lib.current_stream(dev),
     )
-    _lib.check(status, "msgl_paged_decode")
+    if new_kv is None:
+        status = lib.msgl_paged_decode(_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool), *common)
+        _lib.check(status, "msgl_paged_decode")
+    else:
+        k_new, v_new, out_loc = new_kv
+        if k_new.shape != (b, hkv, d) or v_new.shape != (b, hkv, d) or out_loc.shape != (b,):
+            raise ValueError("k_new/v_new must be [B, Hkv, D] and out_loc [B]")
+        if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+            raise ValueError("k_new/v_new must share q's dtype")
+        for name, t in (("k_new", k_new), ("v_new", v_new)):
+            _check_device(name, t, dev)
+        _check_index("out_loc", out_loc, dev)
+        status = lib.msgl_paged_decode_store(
+            _lib.ptr(q), _lib.ptr(k_new), _lib.ptr(v_new), _lib.ptr(out_loc), _lib.ptr(k_pool), _lib.ptr(v_pool),
+            *common,
+        )
+        _lib.check(status, "msgl_paged_decode_store")
     return out
 
 

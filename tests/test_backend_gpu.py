@@ -118,3 +118,41 @@ def test_prefill_then_decode_through_backend(cuda_device):
             assert_close(o, ref, dt, f"backend {phase} layer {layer}")
         for r in reqs:
             r.complete_one()
+
+
+def test_fused_and_eager_store_agree(cuda_device):
+    """The backend's fused decode store gives the same outputs and pool bits as
+    the eager store_kv + forward order, and a pool read in between sees the store."""
+    dt = torch.bfloat16
+    outs, pools = [], []
+    for fuse in (True, False):
+        cfg = ModelConfig(num_qo_heads=16, num_kv_heads=8, head_dim=128, num_layers=2)
+        kv = MHAKVCache(2, 4096, 8, 128, dt, cuda_device)
+        table = np.zeros((4, 512), dtype=np.int32)
+        backend = create_attention_backend("hip", cfg, kv, table)
+        backend.fuse_decode_store = fuse
+        free = np.random.default_rng(3).permutation(4096).astype(np.int32)
+        reqs = [Req(input_ids=np.zeros(n + 1, np.int32), table_idx=i, cached_len=n) for i, n in enumerate([9, 200])]
+        free = oracle.allocate_paged(table, free, [0, 1], [0, 0], [9, 200], 1)
+        free = oracle.allocate_paged(table, free, [0, 1], [9, 200], [10, 201], 1)
+        for layer in range(2):
+            kv.k[layer].copy_(randn(kv.k[layer].shape, 5 + layer, dt).to(cuda_device))
+            kv.v[layer].copy_(randn(kv.v[layer].shape, 7 + layer, dt).to(cuda_device))
+        pos, out_loc = oracle.prepare_batch_indices(table, [0, 1], [9, 200], [10, 201])
+        batch = Batch(reqs=reqs, phase="decode")
+        batch.out_loc = i32(out_loc, cuda_device)
+        backend.prepare_metadata(batch)
+        res = []
+        for layer in range(2):
+            q = randn((2, 16, 128), 30 + layer, dt).to(cuda_device)
+            k = randn((2, 8, 128), 40 + layer, dt).to(cuda_device)
+            v = randn((2, 8, 128), 50 + layer, dt).to(cuda_device)
+            kv.store_kv(k, v, batch.out_loc, layer)
+            if layer == 1:  # a reader between store and forward must see the new rows
+                assert torch.equal(kv.k_cache(1)[batch.out_loc.long()], k)
+            res.append(backend.forward(q, k, v, layer, batch))
+        torch.cuda.synchronize()
+        outs.append(torch.stack(res))
+        pools.append(torch.stack([kv.k_cache(0), kv.v_cache(0), kv.k_cache(1), kv.v_cache(1)]))
+    assert torch.equal(outs[0], outs[1])
+    assert torch.equal(pools[0].view(torch.int16), pools[1].view(torch.int16))

@@ -45,6 +45,7 @@ def test_abi_version_and_sizes():
         1, 16, 8, 128, 64)
     assert 1 <= lib.msgl_paged_decode_default_splits(128, 8, 2048) <= 64
     assert lib.msgl_paged_decode_default_splits(1, 8, 32768) == 64
+    assert lib.msgl_paged_decode_default_splits(128, 8, 2048) == 4
     assert lib.msgl_paged_decode_default_splits(1, 8, 100) == 2  # capped by ceil(100 / 64)
 
 

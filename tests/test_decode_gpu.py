@@ -190,3 +190,35 @@ def test_cfg3_long_contexts_page16(cuda_device):
     pick = list(range(0, 24, 3))
     ref = _sampled_ref(q, kp, vp, c, pick, 128**-0.5, page_size=16)
     assert_close(out[pick], ref, dt, "cfg3 sampled")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_fused_store_matches_two_calls(cuda_device, dtype, splits):
+    """msgl_paged_decode_store == msgl_store_kv + msgl_paged_decode, bit for bit,
+    even when the new tokens' slots hold NaN before the store."""
+    dt = DTYPES[dtype]
+    lens = [1, 2, 17, 64, 65, 300, 1000]
+    c = workloads.decode_case_from_lens(lens, num_slots=4096, seed=21)
+    kp, vp = _pools(4096, 8, 128, dt, 900, cuda_device)
+    loc = i32(c.out_loc, cuda_device)
+    kp[loc.long()] = float("nan")
+    vp[loc.long()] = float("nan")
+    q = randn((len(lens), 16, 128), 902, dt).to(cuda_device)
+    kn = randn((len(lens), 8, 128), 903, dt).to(cuda_device)
+    vn = randn((len(lens), 8, 128), 904, dt).to(cuda_device)
+    indptr, indices = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    kp2, vp2 = kp.clone(), vp.clone()
+    print(f"case fused-store {dtype} splits={splits}", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, indptr, indices, 128**-0.5, max_splits=splits,
+                                     new_kv=(kn, vn, loc))
+    ops.store_kv(kn, vn, loc, kp2, vp2)
+    ref_out = ops.paged_decode_attention(q, kp2, vp2, indptr, indices, 128**-0.5, max_splits=splits)
+    torch.cuda.synchronize()
+    assert torch.equal(kp.view(torch.int16 if dt != torch.float32 else torch.int32),
+                       kp2.view(torch.int16 if dt != torch.float32 else torch.int32))
+    assert torch.equal(vp.view(torch.int16 if dt != torch.float32 else torch.int32),
+                       vp2.view(torch.int16 if dt != torch.float32 else torch.int32))
+    assert torch.equal(out, ref_out)
+    ref = oracle.paged_decode(to_np64(q), to_np64(kp2), to_np64(vp2), c.kv_indptr, c.kv_indices, 128**-0.5)
+    assert_close(out, ref, dt, f"fused store {dtype}")
