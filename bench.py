@@ -44,6 +44,8 @@ def parse_args():
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="first copy 1 GiB device-to-device 3 times (reference kernel for HBM byte counters)")
     return ap.parse_args()
 
 
@@ -116,6 +118,13 @@ def main():
     from minisgl_hip import ops, workloads
 
     dev = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     c = workloads.decode_case(BATCH, LO, HI, POOL, 1, seed=0)
     dec_bytes = workloads.decode_bytes(c.lens, HQ, HKV, D, 2)
     store_bytes = BATCH * HKV * D * 2 * 2 * 2  # K and V rows, read + written
