@@ -15,6 +15,7 @@
  *                            (semantics of attention/naive.py:50-60 forward_decode)
  *   msgl_paged_decode_store  kvcache/pool.py:47-50 + attention/metal.py:112-131 in one launch
  *   msgl_prefill_ragged      attention/base.py:85-105     BaseAttnBackend._forward_prefill
+ *                            (+ _default_splits, _workspace_size)
  *
  * Layouts (identical to the reference, no transposes at the boundary):
  *   q, out   [T, Hq, D]   row-major, dtype `dtype`
@@ -120,27 +121,51 @@ int msgl_paged_decode_store(const void* q, const void* k_new, const void* v_new,
                             int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Key-range splits for msgl_prefill_ragged: enough workgroups for the 256-CU
+ * device, each query block's keys cut into at most this many chunks of at
+ * least 256 keys. max_seq_len (max_i L_i, 0 = unknown) caps the count.
+ * No reference counterpart (MLX runs one SDPA per request).
+ */
+int32_t msgl_prefill_default_splits(int32_t num_reqs, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                    int32_t max_extend_len, int32_t max_seq_len);
+
+/* Bytes of workspace msgl_prefill_ragged needs for max_splits (0 when
+ * max_splits <= 1): fp32 (m, l) and unnormalised O per chunk and query row. */
+int64_t msgl_prefill_workspace_size(int32_t num_tokens, int32_t num_qo_heads, int32_t head_dim, int32_t max_splits);
+
+/*
  * Ragged chunked-prefill attention over a paged pool, one launch per batch.
  * Replaces attention/base.py:85-105 (BaseAttnBackend._forward_prefill, a
  * per-request MLX SDPA loop).
  *
  *   q          [T, Hq, D] packed extend tokens; request i owns rows
- *              q_indptr[i] .. q_indptr[i+1]-1 (E_i rows)
+ *              q_indptr[i] .. q_indptr[i+1]-1 (E_i rows); T = num_tokens =
+ *              q_indptr[R]
  *   kv_indptr  offsets into kv_indices ([R+1]; with seq_lens only [R] read)
  *   kv_indices slots (page ids when page_size > 1) of request i's full KV:
  *              the cached prefix followed by this step's E_i rows, which the
  *              caller stored with msgl_store_kv first
  *   seq_lens   [R] L_i = P_i + E_i, or NULL (L_i = kv_indptr[i+1]-kv_indptr[i])
  *   max_extend_len  max_i E_i (sizes the grid)
+ *   max_seq_len     max_i L_i, or 0 if unknown: with max_splits > 1 the key
+ *              chunk length is ceil(max_seq_len / max_splits) (>= 256) for the
+ *              whole batch, so only long query blocks are split; with 0 every
+ *              block is cut evenly. Only the speed depends on it.
+ *   scale      softmax scale, > 0 (attention/base.py:45: head_dim^-0.5)
+ *   max_splits chunks per query block's key range, 1..16 (bf16/fp16; fp32
+ *              always runs one pass); > 1 needs
+ *              msgl_prefill_workspace_size(num_tokens, Hq, D, max_splits) bytes
+ *              of 256-byte aligned workspace
  *   out        [T, Hq, D]
  * Query t of request i sees keys j <= P_i + t (MLX's bottom-right causal
  * mask, docs/04-attention.md:35-36); E_i <= L_i is required.
  */
 int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, const int32_t* q_indptr,
                         const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
-                        int32_t num_reqs, int32_t max_extend_len, int32_t num_qo_heads, int32_t num_kv_heads,
-                        int32_t head_dim, int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
-                        void* out, void* stream);
+                        int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                        int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                        int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
+                        void* workspace, int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

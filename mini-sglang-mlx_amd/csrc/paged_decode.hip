@@ -475,6 +475,12 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p,
   }
 }
 
+// Wavefronts per workgroup (kv heads handled by one workgroup). Small
+// workgroups let a CU start new work as soon as any wave finishes.
+#ifndef MSGL_DECODE_WAVES_PER_WG
+#define MSGL_DECODE_WAVES_PER_WG 4
+#endif
+
 template <typename T, int D, int G>
 static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
   const int nwaves = p.hkv < MSGL_DECODE_WAVES_PER_WG ? p.hkv : MSGL_DECODE_WAVES_PER_WG;

@@ -7,21 +7,48 @@
 // (docs/04-attention.md:35-36): query t sees key j iff j <= P_i + t. With
 // E_i == 1 the mask keeps every key (attention/base.py:103, mask=None).
 //
-// Design (flash-attention forward, MFMA throughout):
-//  * Workgroup = (request, kv head, block of query rows); query rows are
-//    (token, grouped head) pairs, so the G query heads of one kv head share
-//    every K/V tile (GQA). 4 wavefronts x 16 query rows each.
-//  * Per iteration a 32-key tile is gathered from the pool through the slot
-//    indices into LDS: K row-major (A operand of S^T = K Q^T), V transposed
-//    (B operand of O = P V) so the key dimension is contiguous per lane.
+// Query rows are (token, grouped head) pairs, so the G query heads of one kv
+// head share every K/V tile (GQA). A workgroup owns one block of query rows
+// of one (request, kv head) and one contiguous range of that block's keys.
+//
+// bf16 / fp16 (prefill16_kernel), the serving path:
+//  * 4 wavefronts x 32 query rows (16 for head_dim 256): two 16-row MFMA
+//    column blocks per wavefront share every K fragment and every V operand.
+//  * 32-key K and V tiles are gathered from the pool straight into LDS with
+//    gfx950's global_load_lds_dwordx4 (16 bytes per lane, no register
+//    staging) into a ring of NS stages, NS-1 tiles ahead of the compute. The
+//    wait for a tile is an explicit vmcnt on the issuing wavefront plus one
+//    barrier, so later tiles stay in flight. Slot indices for up to 1024 keys
+//    are staged in LDS first, so no other global load sits in the loop.
+//  * Rows are stored unpadded with an XOR swizzle of their 16-byte chunks
+//    (chunk c of row r lives at c ^ swz(r)); the K operand reads (16 rows,
+//    same chunk) and the transposing V reads (4 rows x 2 chunks per 16 lanes)
+//    are bank-conflict free on the 64-bank LDS.
 //  * S^T = K Q^T with v_mfma_f32_16x16x32_{bf16,f16}: lane (query col l%16,
 //    key group l/16) holds 4 keys of each 16-key tile, which is exactly the A
 //    operand layout P needs for O += P V (converted in registers, no shuffle).
-//    fp32 uses v_mfma_f32_16x16x4f32 and row-major V.
-//  * Online softmax per query row in the exp2 domain; row max/sum across the 4
-//    key groups by two xor shuffles; per-row rescale factors are broadcast to
-//    the accumulator layout with ds_bpermute.
-//  * Causal tiles past a block's last visible key are never loaded.
+//    The B operand of P V (keys contiguous per lane) is read from the
+//    row-major V tile with ds_read_b64_tr_b16.
+//  * Online softmax per query row in the exp2 domain, scores scaled inside
+//    the exponent's FMA.
+//  * Split-K: a block's visible key range [0, kv_end) is cut into at most
+//    `splits` chunks of one batch-wide length (ceil(max_seq_len / splits),
+//    at least 256 keys), so only long blocks are split and every workgroup's
+//    key loop is about equally short. A block with one chunk writes the output
+//    directly; otherwise each chunk writes (m, l, unnormalised O) in fp32 to
+//    the workspace and prefill_merge_kernel combines them.
+//  * Online softmax with a lazily moved reference maximum (see the loop).
+//  * Workgroups are ordered (kv head, request, chunk, block) and remapped
+//    over the 8 XCDs (hardware dispatches workgroup i to XCD i % 8) so that
+//    each XCD takes a contiguous range: the blocks sharing a K/V chunk share
+//    one L2, and with 8 kv heads each XCD serves one head.
+//
+// fp32 (prefill_f32_kernel): one pass per block, 4 wavefronts x 16 rows,
+// register-staged gather into padded LDS tiles, v_mfma_f32_16x16x4f32.
+//
+// Causal tiles past a block's last visible key are never loaded.
+#include <algorithm>
+
 #include "msgl_common.h"
 
 namespace msgl {
@@ -29,9 +56,11 @@ namespace msgl {
 namespace {
 
 constexpr float kLog2eP = 1.4426950408889634f;
-constexpr int KT = 32;      // keys per iteration
-constexpr int NWAVE = 4;    // wavefronts per workgroup
-constexpr int QROWS = 16;   // query rows per wavefront
+constexpr int KT = 32;           // keys per tile
+constexpr int NWAVE = 4;         // wavefronts per workgroup
+constexpr int kWin = 1024;       // keys whose slots are staged in LDS at a time
+constexpr int kMinChunk = 256;   // smallest key range given its own workgroup
+constexpr int kMaxSplits = 16;
 
 struct PrefillParams {
   const void* q;
@@ -42,8 +71,15 @@ struct PrefillParams {
   const int32_t* kv_indices;
   const int32_t* seq_lens;
   void* out;
+  float* part_o;    // [splits][num_tokens][hq][D]
+  float2* part_ml;  // [splits][num_tokens][hq]
   int64_t num_slots;
   int hq, hkv, page_size;
+  int num_reqs, num_tokens;
+  int splits;     // key chunks per block (grid dimension)
+  int chunk_len;  // keys per chunk, 0 = per block
+  int nqb;      // query blocks per request (grid dimension)
+  int items;    // workgroups with a logical index
   float scale_log2;
 };
 
@@ -57,71 +93,476 @@ __device__ __forceinline__ int64_t kv_slot(const PrefillParams& p, int start, in
   return (s >= 0 && s < p.num_slots) ? s : 0;
 }
 
-template <typename T>
-struct PF;
+// Keys a block of query tokens [qb, qb + bq) can see.
+__device__ __forceinline__ int block_kv_end(int L, int E, int qb, int bq) {
+  return min(L, L - E + min(E, qb + bq));
+}
 
-// 16-bit types: K row-major [KT][D+8], V transposed [D][KT+4] in LDS.
-template <typename T>
-struct PF16 {
-  static constexpr int VEC = 8;
-  template <int D>
-  static constexpr int k_stride() { return D + 8; }       // elements
-  static constexpr int vt_stride() { return KT + 4; }     // elements
-  template <int D>
-  static constexpr int lds_bytes() { return (KT * (D + 8) + D * (KT + 4)) * 2; }
-};
+// Split of [0, kv_end) into n <= splits chunks of clen keys (a multiple of
+// the tile; the last chunk takes the rest), used identically by the attention
+// and merge kernels. With a batch-wide chunk length (from the longest
+// sequence) only long blocks are split; without one each block is cut evenly.
+__device__ __forceinline__ void chunk_geometry(int kv_end, int splits, int chunk_len, int& n, int& clen) {
+  if (chunk_len > 0) {
+    clen = chunk_len;
+  } else {
+    const int n0 = max(1, min(splits, (kv_end + kMinChunk - 1) / kMinChunk));
+    clen = ((kv_end + n0 - 1) / n0 + KT - 1) / KT * KT;
+  }
+  n = min(splits, (kv_end + clen - 1) / clen);
+}
 
+#define MSGL_LDS __attribute__((address_space(3)))
+typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+typedef __fp16 f16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+
+// ds_read_b64_tr_b16: within each 16-lane group, source lane j's 4 elements
+// X[j][0..3] are redistributed so lane i receives Y[i][e] = X[4e + i/4][i%4]
+// (lane-layout measured on gfx950). If source lane j points at row key_{j/4},
+// columns c0 + 4*(j%4), lane i receives rows key_0..key_3 of column c0 + i.
+template <typename T>
+__device__ __forceinline__ uint2 lds_read_tr16(const uint8_t* p);
 template <>
-struct PF<bf16_t> : PF16<bf16_t> {
+__device__ __forceinline__ uint2 lds_read_tr16<bf16_t>(const uint8_t* p) {
+  MSGL_LDS bf16x4_t* lp = (MSGL_LDS bf16x4_t*)(p);
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4bf16(lp));
+}
+template <>
+__device__ __forceinline__ uint2 lds_read_tr16<f16_t>(const uint8_t* p) {
+  MSGL_LDS f16x4_t* lp = (MSGL_LDS f16x4_t*)(p);
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(lp));
+}
+
+// 16 bytes per lane from global memory into LDS at m0 + 16 * lane. Issued as
+// inline assembly so the compiler does not drain every outstanding transfer
+// before the next LDS read; the caller waits with vm_wait.
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
+  // m0 is reserved by the compiler, so it cannot be listed as clobbered; the
+  // kernels using this helper have no other m0 user.
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+template <typename T>
+struct MMA16;
+template <>
+struct MMA16<bf16_t> {
   __device__ __forceinline__ static f32x4 mma(const u32x4& a, const u32x4& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
   }
+  // v_cvt_pk_bf16_f32: round-to-nearest-even, like f32_to_bf16
   __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
-    return (uint32_t)f32_to_bf16(lo) | ((uint32_t)f32_to_bf16(hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
   }
 };
-
 template <>
-struct PF<f16_t> : PF16<f16_t> {
+struct MMA16<f16_t> {
   __device__ __forceinline__ static f32x4 mma(const u32x4& a, const u32x4& b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
                                                   0, 0);
   }
   __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
-    return (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
-           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
   }
 };
 
-template <>
-struct PF<float> {
-  static constexpr int VEC = 4;
-  template <int D>
-  static constexpr int k_stride() { return D + 4; }
-  template <int D>
-  static constexpr int lds_bytes() { return 2 * KT * (D + 4) * 4; }
+// Geometry of the 16-bit kernel for one head_dim.
+template <int D>
+struct G16 {
+  static constexpr int RB = D <= 128 ? 2 : 1;       // 16-row column blocks per wavefront
+  static constexpr int ROWS = NWAVE * 16 * RB;      // query rows per workgroup
+  static constexpr int RBYTES = D * 2;              // bytes per K/V row
+  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int SWZ = CPR >= 16 ? 15 : CPR - 1;
+  static constexpr int TILE_BYTES = KT * RBYTES;    // K (or V) tile
+  static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+  // Ring depth and the occupancy the register budget is built for: two
+  // workgroups per CU at head_dim 128 (2 x 68 KiB of the 160 KiB LDS,
+  // <= 256 VGPRs), three at 64.
+  static constexpr int NS = D <= 128 ? 4 : 2;
+  static constexpr int WAVES = D <= 64 ? 3 : 2;
+  static constexpr int IPW = TILE_BYTES / 1024 / NWAVE;  // 1 KiB transfers per wavefront, each of K and V
+  static constexpr int LDS_BYTES = NS * STAGE_BYTES + kWin * 4;
+  static_assert(TILE_BYTES % (1024 * NWAVE) == 0, "a tile must split evenly over the wavefronts");
 };
 
+// XOR swizzle of a row's 16-byte chunks: a bijection on r % 16, so 16
+// consecutive rows place one logical chunk in 16 different bank groups, and
+// rows 4g..4g+3 x chunks {2t, 2t+1} land in 8 different ones.
+__device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | (((r >> 2) & 1) << 3) | ((r >> 3) & 1); }
+
 template <typename T, int D, int G>
-__global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
-  constexpr int ES = sizeof(T);
-  constexpr int VEC = PF<T>::VEC;
-  constexpr int ROWS = NWAVE * QROWS;   // query rows per workgroup
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAVES))) void prefill16_kernel(
+    PrefillParams p) {
+  using Geo = G16<D>;
+  constexpr int RB = Geo::RB;
+  constexpr int ROWS = Geo::ROWS;
   static_assert(ROWS % G == 0, "group must divide the row block");
-  constexpr int BQ = ROWS / G;          // query tokens per workgroup
-  constexpr int NDT = D / 16;           // 16-wide output column tiles
-  constexpr int KS = PF<T>::template k_stride<D>();
+  constexpr int BQ = ROWS / G;  // query tokens per workgroup
+  constexpr int NQF = D / 32;   // 32-wide d slices of the S^T product
+  constexpr int NDT = D / 16;   // 16-wide output column tiles
+  constexpr int NS = Geo::NS;
+  constexpr int IPW = Geo::IPW;
+  constexpr int RBYTES = Geo::RBYTES;
+  constexpr int CPR = Geo::CPR;
+  constexpr int SWZ = Geo::SWZ;
 
   extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
-  T* Ks = reinterpret_cast<T*>(smem);                 // [KT][KS]
-  T* Vs = Ks + KT * KS;                               // 16-bit: Vt[D][KT+4]; fp32: V[KT][KS]
+  int* slots = reinterpret_cast<int*>(smem + NS * Geo::STAGE_BYTES);
+  const uint32_t lds0 = (uint32_t)(uintptr_t)((MSGL_LDS uint8_t*)smem);
+
+  // ---- logical work item (XCD-contiguous ranges) ----
+  const int per_xcd = gridDim.x >> 3;
+  const int lid = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
+  if (lid >= p.items) return;
+  const int qblk = lid % p.nqb;
+  int rest = lid / p.nqb;
+  const int split = rest % p.splits;
+  rest /= p.splits;
+  const int req = rest % p.num_reqs;
+  const int kvh = rest / p.num_reqs;
+
+  const int q0 = p.q_indptr[req];
+  const int E = p.q_indptr[req + 1] - q0;
+  const int qb = qblk * BQ;
+  if (qb >= E) return;
+  const int kv_start = p.kv_indptr[req];
+  const int L = p.seq_lens ? p.seq_lens[req] : (p.kv_indptr[req + 1] - kv_start);
+  const int P = L - E;
+  const int kv_end = block_kv_end(L, E, qb, BQ);
+  int nchunks, clen;
+  chunk_geometry(kv_end, p.splits, p.chunk_len, nchunks, clen);
+  if (split >= nchunks) return;
+  const int c0 = split * clen;
+  const int c1 = split == nchunks - 1 ? kv_end : c0 + clen;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int col = lane & 15;   // S^T column = query row within the wave tile
-  const int grp = lane >> 4;   // key group
+  const int col = lane & 15;  // S^T column = query row within a 16-row block
+  const int grp = lane >> 4;  // key group
+
+  // this lane's query rows (one per column block), clamped into range so every
+  // row sees key 0; rows past E are computed, not stored
+  int limit[RB];
+  u32x4 qf[RB][NQF];
+#pragma unroll
+  for (int b = 0; b < RB; ++b) {
+    const int row = (wave * RB + b) * 16 + col;
+    const int tok = min(qb + row / G, E - 1);
+    limit[b] = P + tok;
+    const uint8_t* qrow =
+        reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * RBYTES;
+#pragma unroll
+    for (int j = 0; j < NQF; ++j) qf[b][j] = ld16(qrow + (32 * j + 8 * grp) * 2);
+  }
+  // smallest visible-key limit of each column block (its first row, lane 0)
+  int lim_lo[RB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b) lim_lo[b] = __builtin_amdgcn_readfirstlane(limit[b]);
+  // Q must have arrived before the key loop: otherwise the compiler's wait for
+  // it lands inside the loop (its wait analysis merges the loop entry), where a
+  // vmcnt would also drain the LDS transfers in flight.
+#pragma unroll
+  for (int b = 0; b < RB; ++b)
+#pragma unroll
+    for (int j = 0; j < NQF; ++j) asm volatile("" ::"v"(qf[b][j]));
+
+  f32x4 acc[RB][NDT];
+  float m_run[RB], l_run[RB];
+#pragma unroll
+  for (int b = 0; b < RB; ++b) {
+    m_run[b] = -INFINITY;
+    l_run[b] = 0.f;
+#pragma unroll
+    for (int t = 0; t < NDT; ++t) acc[b][t] = f32x4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  const uint8_t* kp = reinterpret_cast<const uint8_t*>(p.k_pool);
+  const uint8_t* vp = reinterpret_cast<const uint8_t*>(p.v_pool);
+  const int64_t row_stride = (int64_t)p.hkv * RBYTES;
+  const int64_t head_off = (int64_t)kvh * RBYTES;
+
+  // Tile t of the window into ring stage st: this wavefront's IPW transfers of
+  // K and of V. Transfer qi covers LDS bytes [qi KiB, (qi+1) KiB) of the tile:
+  // lane l fills physical chunk (qi*64 + l) % CPR of row (qi*64 + l) / CPR with
+  // logical chunk pc ^ swz(row). Rows past the window repeat its last key.
+  auto issue = [&](int t, int st, int nw) {
+    const uint32_t sb = lds0 + st * Geo::STAGE_BYTES;
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) {
+      const int qi = wave + NWAVE * i;
+      const int flat = qi * 64 + lane;
+      const int r = flat / CPR;
+      const int c = (flat % CPR) ^ (swz(r) & SWZ);
+      const int key = min(t * KT + r, nw - 1);
+      const int64_t off = (int64_t)slots[key] * row_stride + head_off + c * 16;
+      const uint32_t lk = __builtin_amdgcn_readfirstlane(sb + qi * 1024);
+      dma16(kp + off, lk);
+      dma16(vp + off, lk + Geo::TILE_BYTES);
+    }
+  };
+  // Wait until this wavefront's transfers of a tile have landed, `after` tiles
+  // having been issued behind it.
+  auto wait_tile = [&](int after) {
+    if (after <= 0) {
+      vm_wait<0>();
+    } else if (after == 1) {
+      vm_wait<2 * IPW>();
+    } else {
+      vm_wait<4 * IPW>();
+    }
+  };
+
+  for (int w0 = c0; w0 < c1; w0 += kWin) {
+    const int nw = min(kWin, c1 - w0);
+    const int ntiles = (nw + KT - 1) / KT;
+    __syncthreads();  // every wavefront is done with the previous window
+    for (int i = tid; i < nw; i += 256) slots[i] = (int)kv_slot(p, kv_start, w0 + i);
+    __syncthreads();
+#pragma unroll
+    for (int s = 0; s < NS - 1; ++s)
+      if (s < ntiles) issue(s, s, nw);
+
+    for (int t = 0; t < ntiles; ++t) {
+      wait_tile(min(NS - 2, ntiles - 1 - t));
+      __syncthreads();  // tile t visible to all; everyone is done with tile t-1's stage
+      if (t + NS - 1 < ntiles) issue(t + NS - 1, (t + NS - 1) % NS, nw);
+
+      const uint8_t* Kb = smem + (t % NS) * Geo::STAGE_BYTES;
+      const uint8_t* Vb = Kb + Geo::TILE_BYTES;
+      const int kbase = w0 + t * KT;
+      const int kend = w0 + nw;
+
+      // ---- S^T = K Q^T for two 16-key halves, each K fragment feeding RB blocks ----
+      f32x4 s[2][RB];
+#pragma unroll
+      for (int kt = 0; kt < 2; ++kt) {
+        const int r = kt * 16 + col;
+        const uint8_t* krow = Kb + r * RBYTES;
+        const int sw = swz(r) & SWZ;
+#pragma unroll
+        for (int b = 0; b < RB; ++b) s[kt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NQF; ++j) {
+          const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (((4 * j + grp) ^ sw) << 4));
+#pragma unroll
+          for (int b = 0; b < RB; ++b) s[kt][b] = MMA16<T>::mma(a, qf[b][j], s[kt][b]);
+        }
+      }
+
+      // ---- online softmax per column block; P packed as the A operand ----
+      const bool tail = kbase + KT > kend;  // the tile runs past the key range
+      u32x4 pa[RB];
+#pragma unroll
+      for (int b = 0; b < RB; ++b) {
+        // raw scores; masking only where some row of the block misses a key
+        float x[2][4];
+        float mloc = -INFINITY;
+        if (!tail && kbase + KT - 1 <= lim_lo[b]) {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              x[kt][i] = s[kt][b][i];
+              mloc = fmaxf(mloc, x[kt][i]);
+            }
+        } else {
+#pragma unroll
+          for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int key = kbase + kt * 16 + 4 * grp + i;
+              const bool vis = key <= limit[b] && key < kend;
+              x[kt][i] = vis ? s[kt][b][i] : -INFINITY;
+              mloc = fmaxf(mloc, x[kt][i]);
+            }
+        }
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
+        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
+        // Lazy rescale (scale > 0, so the raw max orders like the scaled one):
+        // a row's reference m_run (log2 domain) moves only when its max exceeds
+        // it by more than 8, so P <= 2^8 and most tiles leave the accumulators
+        // alone. Exact up to rounding: P, l and O share the reference.
+        const float mcand = mloc * p.scale_log2;
+        const bool grow = mcand > m_run[b] + 8.f;
+        if (__ballot(grow) != 0) {
+          const float m_new = grow ? mcand : m_run[b];
+          const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[b] - m_new) : 1.f;
+          l_run[b] *= alpha;
+          m_run[b] = m_new;
+          // accumulator row 4*grp+i takes the factor of S^T column 4*grp+i
+          float arow[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * grp + i);
+#pragma unroll
+          for (int t2 = 0; t2 < NDT; ++t2)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) acc[b][t2][i] *= arow[i];
+        }
+        const float m_use = m_run[b] == -INFINITY ? 0.f : m_run[b];  // a row may see nothing yet
+        float pr[2][4];
+        float lsum = 0.f;
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            pr[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kt][i], p.scale_log2, -m_use));
+            lsum += pr[kt][i];
+          }
+        l_run[b] += lsum;
+        // A operand slot (grp, e<4) = key 4*grp+e, (grp, e>=4) = key 16+4*grp+e-4
+        pa[b][0] = MMA16<T>::pack2(pr[0][0], pr[0][1]);
+        pa[b][1] = MMA16<T>::pack2(pr[0][2], pr[0][3]);
+        pa[b][2] = MMA16<T>::pack2(pr[1][0], pr[1][1]);
+        pa[b][3] = MMA16<T>::pack2(pr[1][2], pr[1][3]);
+      }
+
+      // ---- O += P V: source lane col reads row 4*grp + col/4 (+16), columns
+      //      16t + 4*(col%4) .. +3, i.e. logical chunk 2t + (col%4)/2, half col%2 ----
+      const int rlo = 4 * grp + (col >> 2);
+      const int vsw = swz(rlo) & SWZ;  // rlo + 16 has the same swizzle
+      const uint8_t* vrow = Vb + rlo * RBYTES + ((col & 1) << 3);
+#pragma unroll
+      for (int t2 = 0; t2 < NDT; ++t2) {
+        const int off = ((2 * t2 + ((col >> 1) & 1)) ^ vsw) << 4;
+        const uint2 lo = lds_read_tr16<T>(vrow + off);
+        const uint2 hi = lds_read_tr16<T>(vrow + 16 * RBYTES + off);
+        const u32x4 bop = {lo.x, lo.y, hi.x, hi.y};
+#pragma unroll
+        for (int b = 0; b < RB; ++b) acc[b][t2] = MMA16<T>::mma(pa[b], bop, acc[b][t2]);
+      }
+    }
+  }
+
+  // ---- results: accumulator row 4*grp+i of block b is WG row (wave*RB+b)*16 + 4*grp + i ----
+#pragma unroll
+  for (int b = 0; b < RB; ++b) {
+    float l = l_run[b];
+    l += __shfl_xor(l, 16);
+    l += __shfl_xor(l, 32);
+    const int rbase = (wave * RB + b) * 16;
+    if (nchunks == 1) {
+      const float inv = 1.f / l;
+      T* out = reinterpret_cast<T*>(p.out);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = rbase + 4 * grp + i;
+        const int tok = qb + row / G;
+        const float rinv = __shfl(inv, 4 * grp + i);
+        if (tok < E) {
+          T* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
+#pragma unroll
+          for (int t2 = 0; t2 < NDT; ++t2) orow[t2 * 16 + col] = from_f32<T>(acc[b][t2][i] * rinv);
+        }
+      }
+    } else {
+      const int64_t base = (int64_t)split * p.num_tokens;
+      if (grp == 0) {
+        const int row = rbase + col;
+        const int tok = qb + row / G;
+        if (tok < E && q0 + tok < p.num_tokens)
+          p.part_ml[(base + q0 + tok) * p.hq + kvh * G + row % G] = make_float2(m_run[b], l);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int row = rbase + 4 * grp + i;
+        const int tok = qb + row / G;
+        if (tok < E && q0 + tok < p.num_tokens) {  // the workspace holds num_tokens rows
+          float* orow = p.part_o + ((base + q0 + tok) * p.hq + kvh * G + row % G) * D;
+#pragma unroll
+          for (int t2 = 0; t2 < NDT; ++t2) orow[t2 * 16 + col] = acc[b][t2][i];
+        }
+      }
+    }
+  }
+}
+
+// Combines the chunks of every query row whose block was split: one thread
+// per 4 output columns of one (token, head).
+template <typename T, int D>
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p, int bq) {
+  constexpr int TPH = D / 4;
+  constexpr int HPB = 256 / TPH;
+  const int tk = blockIdx.x;
+  const int h = blockIdx.y * HPB + threadIdx.x / TPH;
+  const int d = (threadIdx.x % TPH) * 4;
+  if (h >= p.hq) return;
+  // request owning token tk: the last r with q_indptr[r] <= tk
+  int lo = 0, hi = p.num_reqs - 1;
+  while (lo < hi) {
+    const int mid = (lo + hi + 1) >> 1;
+    if (p.q_indptr[mid] <= tk) lo = mid; else hi = mid - 1;
+  }
+  const int q0 = p.q_indptr[lo];
+  const int E = p.q_indptr[lo + 1] - q0;
+  const int L = p.seq_lens ? p.seq_lens[lo] : (p.kv_indptr[lo + 1] - p.kv_indptr[lo]);
+  const int tok = tk - q0;
+  if (tok < 0 || tok >= E) return;
+  const int kv_end = block_kv_end(L, E, tok / bq * bq, bq);
+  int n, clen;
+  chunk_geometry(kv_end, p.splits, p.chunk_len, n, clen);
+  if (n <= 1) return;  // written by the attention kernel
+  const int64_t stride = (int64_t)p.num_tokens * p.hq;
+  const int64_t idx = (int64_t)tk * p.hq + h;
+  float M = -INFINITY;
+  for (int c = 0; c < n; ++c) M = fmaxf(M, p.part_ml[c * stride + idx].x);
+  float o[4] = {0.f, 0.f, 0.f, 0.f};
+  float lsum = 0.f;
+  for (int c = 0; c < n; ++c) {
+    const float2 ml = p.part_ml[c * stride + idx];
+    const float w = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - M);
+    lsum += ml.y * w;
+    const float4 v = *reinterpret_cast<const float4*>(p.part_o + (c * stride + idx) * D + d);
+    o[0] += w * v.x;
+    o[1] += w * v.y;
+    o[2] += w * v.z;
+    o[3] += w * v.w;
+  }
+  const float inv = 1.f / lsum;
+  T* dst = reinterpret_cast<T*>(p.out) + idx * D + d;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(o[e] * inv);
+}
+
+// ---------------------------------------------------------------------------
+// fp32: one pass per block, register-staged gather
+// ---------------------------------------------------------------------------
+constexpr int QROWS32 = 16;  // query rows per wavefront
+
+template <int D>
+struct G32 {
+  static constexpr int KS = D + 4;  // padded row stride (floats)
+  static constexpr int BUF_BYTES = 2 * KT * KS * 4;
+  static constexpr int NBUF = 2 * BUF_BYTES <= 65536 ? 2 : 1;
+  static constexpr int LDS_BYTES = NBUF * BUF_BYTES;
+};
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
+  constexpr int ROWS = NWAVE * QROWS32;
+  static_assert(ROWS % G == 0, "group must divide the row block");
+  constexpr int BQ = ROWS / G;
+  constexpr int NDT = D / 16;
+  constexpr int KS = G32<D>::KS;
+  constexpr int BUF_BYTES = G32<D>::BUF_BYTES;
+  constexpr int NBUF = G32<D>::NBUF;
+
+  extern __shared__ __attribute__((aligned(16))) uint8_t smem[];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int col = lane & 15;
+  const int grp = lane >> 4;
 
   const int req = blockIdx.y / p.hkv;
   const int kvh = blockIdx.y % p.hkv;
@@ -132,79 +573,99 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
   const int kv_start = p.kv_indptr[req];
   const int Lkv = p.seq_lens ? p.seq_lens[req] : (p.kv_indptr[req + 1] - kv_start);
   const int P = Lkv - E;
-  const int kv_end = min(Lkv, P + min(E, qb + BQ));  // keys this block can see
+  const int kv_end = block_kv_end(Lkv, E, qb, BQ);
 
-  // this lane's query row (as S^T column) and its token (clamped into range so
-  // every row has at least key 0 visible; rows past E are computed, not stored)
-  const int my_row = wave * QROWS + col;
+  const int my_row = wave * QROWS32 + col;
   const int my_tok = min(qb + my_row / G, E - 1);
-  const int my_limit = P + my_tok;  // last visible key
+  const int my_limit = P + my_tok;
   const int my_head = kvh * G + my_row % G;
 
-  // Q fragment (B operand): d = 4*VEC*j + VEC*grp + e
-  constexpr int NQF = D / (4 * VEC);
+  // Q fragment (B operand of 16x16x4): d = 16*j + 4*grp + e
+  constexpr int NQF = D / 16;
   u32x4 qf[NQF];
   {
-    const uint8_t* qrow = reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + my_tok) * p.hq + my_head) * D * ES;
+    const uint8_t* qrow = reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + my_tok) * p.hq + my_head) * D * 4;
 #pragma unroll
-    for (int j = 0; j < NQF; ++j) qf[j] = ld16(qrow + (4 * VEC * j + VEC * grp) * ES);
+    for (int j = 0; j < NQF; ++j) qf[j] = ld16(qrow + (16 * j + 4 * grp) * 4);
   }
 
   f32x4 acc[NDT];
 #pragma unroll
   for (int t = 0; t < NDT; ++t) acc[t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;  // per query row (this lane's column)
+  float m_run = -INFINITY, l_run = 0.f;
 
   const uint8_t* kp = reinterpret_cast<const uint8_t*>(p.k_pool);
   const uint8_t* vp = reinterpret_cast<const uint8_t*>(p.v_pool);
-  const int64_t row_stride = (int64_t)p.hkv * D * ES;
-  const int64_t head_off = (int64_t)kvh * D * ES;
+  const int64_t row_stride = (int64_t)p.hkv * D * 4;
+  const int64_t head_off = (int64_t)kvh * D * 4;
 
-  for (int kt0 = 0; kt0 < kv_end; kt0 += KT) {
-    // ---- gather the key tile into LDS ----
-    __syncthreads();
-    constexpr int CPR = D / VEC;  // 16-byte chunks per row
-    for (int c = tid; c < KT * CPR; c += 256) {
-      const int key = c / CPR, ch = c % CPR;
-      const int j = kt0 + key;
-      u32x4 kv = {0u, 0u, 0u, 0u}, vv = {0u, 0u, 0u, 0u};
-      if (j < kv_end) {
-        const int64_t s = kv_slot(p, kv_start, j);
-        kv = ld16(kp + s * row_stride + head_off + ch * 16);
-        vv = ld16(vp + s * row_stride + head_off + ch * 16);
-      }
-      *reinterpret_cast<u32x4*>(Ks + key * KS + ch * VEC) = kv;
-      if constexpr (ES == 2) {
-        constexpr int VTS = KT + 4;
-        const uint16_t* e16 = reinterpret_cast<const uint16_t*>(&vv);
+  // slots two tiles ahead, rows one tile ahead (registers), compute from LDS
+  constexpr int CPR = D / 4;
+  constexpr int CH = KT * CPR / 256;
+  static_assert((KT * CPR) % 256 == 0, "a tile must split evenly over 256 threads");
+  int nslot[CH];
+  u32x4 kreg[CH], vreg[CH];
+  auto slots_for = [&](int kt0) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) reinterpret_cast<uint16_t*>(Vs)[(ch * 8 + e) * VTS + key] = e16[e];
+    for (int i = 0; i < CH; ++i) {
+      const int j = kt0 + (tid + 256 * i) / CPR;
+      nslot[i] = j < kv_end ? (int)kv_slot(p, kv_start, j) : -1;
+    }
+  };
+  auto gload = [&]() {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int ch = (tid + 256 * i) % CPR;
+      if (nslot[i] >= 0) {
+        const int64_t off = (int64_t)nslot[i] * row_stride + head_off + ch * 16;
+        kreg[i] = ld16(kp + off);
+        vreg[i] = ld16(vp + off);
       } else {
-        *reinterpret_cast<u32x4*>(Vs + key * KS + ch * VEC) = vv;
+        kreg[i] = u32x4{0u, 0u, 0u, 0u};
+        vreg[i] = u32x4{0u, 0u, 0u, 0u};
       }
     }
-    __syncthreads();
+  };
+  auto lstore = [&](int buf) {
+    float* Kb = reinterpret_cast<float*>(smem + buf * BUF_BYTES);
+    float* Vb = Kb + KT * KS;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      const int key = (tid + 256 * i) / CPR, ch = (tid + 256 * i) % CPR;
+      *reinterpret_cast<u32x4*>(Kb + key * KS + ch * 4) = kreg[i];
+      *reinterpret_cast<u32x4*>(Vb + key * KS + ch * 4) = vreg[i];
+    }
+  };
+  slots_for(0);
+  gload();
+  lstore(0);
+  slots_for(KT);
+  __syncthreads();
 
-    // ---- S^T = K Q^T for two 16-key tiles ----
+  int buf = 0;
+  for (int kt0 = 0; kt0 < kv_end; kt0 += KT) {
+    const bool more = kt0 + KT < kv_end;
+    if (more) {
+      gload();
+      slots_for(kt0 + 2 * KT);
+    }
+    const float* Ks = reinterpret_cast<const float*>(smem + buf * BUF_BYTES);
+    const float* Vs = Ks + KT * KS;
+
     f32x4 s[2];
 #pragma unroll
     for (int kt = 0; kt < 2; ++kt) {
       s[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const T* krow = Ks + (kt * 16 + col) * KS;
+      const float* krow = Ks + (kt * 16 + col) * KS;
 #pragma unroll
       for (int j = 0; j < NQF; ++j) {
-        const u32x4 a = *reinterpret_cast<const u32x4*>(krow + 4 * VEC * j + VEC * grp);
-        if constexpr (ES == 2) {
-          s[kt] = PF<T>::mma(a, qf[j], s[kt]);
-        } else {
+        const u32x4 a = *reinterpret_cast<const u32x4*>(krow + 16 * j + 4 * grp);
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[e]), __uint_as_float(qf[j][e]), s[kt], 0,
-                                                         0, 0);
-        }
+        for (int e = 0; e < 4; ++e)
+          s[kt] = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[e]), __uint_as_float(qf[j][e]), s[kt], 0, 0,
+                                                       0);
       }
     }
-    // ---- online softmax for this lane's query row ----
     float x[2][4];
     float mloc = -INFINITY;
 #pragma unroll
@@ -218,7 +679,7 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
       }
     mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
     mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-    const float m_new = fmaxf(m_run, mloc);
+    const float m_new = fmaxf(m_run, mloc);  // key 0 is visible to every row: finite from the first tile
     const float alpha = __builtin_amdgcn_exp2f(m_run - m_new);
     float pr[2][4];
     float lsum = 0.f;
@@ -232,7 +693,6 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
     l_run = l_run * alpha + lsum;
     m_run = m_new;
 
-    // ---- rescale accumulators: row 4*grp+i takes alpha of column 4*grp+i ----
     float arow[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * grp + i);
@@ -241,72 +701,110 @@ __global__ __launch_bounds__(256) void prefill_kernel(PrefillParams p) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) acc[t][i] *= arow[i];
 
-    // ---- O += P V ----
-    if constexpr (ES == 2) {
-      // A operand: slot (grp, e<4) = key 4*grp+e of tile 0, (grp, e>=4) = key 16+4*grp+e-4
-      u32x4 pa;
-      pa[0] = PF<T>::pack2(pr[0][0], pr[0][1]);
-      pa[1] = PF<T>::pack2(pr[0][2], pr[0][3]);
-      pa[2] = PF<T>::pack2(pr[1][0], pr[1][1]);
-      pa[3] = PF<T>::pack2(pr[1][2], pr[1][3]);
-      constexpr int VTS = KT + 4;
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) {
-        const uint16_t* vt = reinterpret_cast<const uint16_t*>(Vs) + (t * 16 + col) * VTS;
-        const uint2 lo = *reinterpret_cast<const uint2*>(vt + 4 * grp);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vt + 16 + 4 * grp);
-        const u32x4 b = {lo.x, lo.y, hi.x, hi.y};
-        acc[t] = PF<T>::mma(pa, b, acc[t]);
+    for (int kt = 0; kt < 2; ++kt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float* vrow = Vs + (kt * 16 + 4 * grp + i) * KS;
+#pragma unroll
+        for (int t = 0; t < NDT; ++t)
+          acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[kt][i], vrow[t * 16 + col], acc[t], 0, 0, 0);
       }
+    if constexpr (NBUF == 2) {
+      if (more) lstore(buf ^ 1);  // the other buffer was last read before the previous barrier
+      __syncthreads();
+      buf ^= 1;
     } else {
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float* vrow = reinterpret_cast<const float*>(Vs) + (kt * 16 + 4 * grp + i) * KS;
-#pragma unroll
-          for (int t = 0; t < NDT; ++t)
-            acc[t] = __builtin_amdgcn_mfma_f32_16x16x4f32(pr[kt][i], vrow[t * 16 + col], acc[t], 0, 0, 0);
-        }
+      __syncthreads();
+      if (more) lstore(0);
+      __syncthreads();
     }
   }
 
-  // ---- normalise and store: acc row 4*grp+i is query row wave*16 + 4*grp + i ----
   l_run += __shfl_xor(l_run, 16);
   l_run += __shfl_xor(l_run, 32);
   const float inv = 1.f / l_run;
-  T* out = reinterpret_cast<T*>(p.out);
+  float* out = reinterpret_cast<float*>(p.out);
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = wave * QROWS + 4 * grp + i;
+    const int row = wave * QROWS32 + 4 * grp + i;
     const int tok = qb + row / G;
     const float rinv = __shfl(inv, 4 * grp + i);
     if (tok < E) {
-      T* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
+      float* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
-      for (int t = 0; t < NDT; ++t) orow[t * 16 + col] = from_f32<T>(acc[t][i] * rinv);
+      for (int t = 0; t < NDT; ++t) orow[t * 16 + col] = acc[t][i] * rinv;
     }
   }
 }
 
+// ---------------------------------------------------------------------------
+// launch
+// ---------------------------------------------------------------------------
+int tokens_per_block16(int head_dim, int group) {
+  const int rows = head_dim <= 128 ? NWAVE * 32 : NWAVE * 16;
+  return rows / group;
+}
+
 template <typename T, int D, int G>
-int launch_prefill(const PrefillParams& p, int num_reqs, int max_extend_len, hipStream_t stream) {
-  constexpr int BQ = NWAVE * QROWS / G;
-  const int qblocks = (max_extend_len + BQ - 1) / BQ;
-  const size_t lds = PF<T>::template lds_bytes<D>();
-  hipLaunchKernelGGL((prefill_kernel<T, D, G>), dim3(qblocks, num_reqs * p.hkv), dim3(256), lds, stream, p);
+int launch16(PrefillParams p, int max_e, hipStream_t stream) {
+  using Geo = G16<D>;
+  constexpr int BQ = Geo::ROWS / G;
+  p.nqb = (max_e + BQ - 1) / BQ;
+  const int64_t items = (int64_t)p.hkv * p.num_reqs * p.splits * p.nqb;
+  if (items > (int64_t)INT32_MAX - 8) {
+    set_error("msgl_prefill_ragged: %lld workgroups exceed the grid limit", (long long)items);
+    return MSGL_ERR_INVALID;
+  }
+  p.items = (int)items;
+  const int grid = (int)((items + 7) / 8 * 8);
+  static bool attr_set = false;  // per process; the attribute is per function
+  if (Geo::LDS_BYTES > 65536 && !attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill16_kernel<T, D, G>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, Geo::LDS_BYTES) != hipSuccess) {
+      set_error("msgl_prefill_ragged: cannot raise the LDS limit to %d bytes", Geo::LDS_BYTES);
+      return MSGL_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((prefill16_kernel<T, D, G>), dim3(grid), dim3(256), Geo::LDS_BYTES, stream, p);
+  MSGL_CHECK_LAUNCH("msgl_prefill_ragged");
+  if (p.splits > 1) {
+    constexpr int HPB = 256 / (D / 4);
+    hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3(p.num_tokens, (p.hq + HPB - 1) / HPB), dim3(256), 0,
+                       stream, p, BQ);
+    MSGL_CHECK_LAUNCH("msgl_prefill_ragged (merge)");
+  }
+  return MSGL_OK;
+}
+
+template <int D, int G>
+int launch32(const PrefillParams& p, int max_e, hipStream_t stream) {
+  constexpr int BQ = NWAVE * QROWS32 / G;
+  const int qblocks = (max_e + BQ - 1) / BQ;
+  hipLaunchKernelGGL((prefill_f32_kernel<D, G>), dim3(qblocks, p.num_reqs * p.hkv), dim3(256), G32<D>::LDS_BYTES,
+                     stream, p);
   MSGL_CHECK_LAUNCH("msgl_prefill_ragged");
   return MSGL_OK;
 }
 
+template <typename T, int D, int G>
+int launch_prefill(const PrefillParams& p, int max_e, hipStream_t s) {
+  if constexpr (sizeof(T) == 4) {
+    return launch32<D, G>(p, max_e, s);
+  } else {
+    return launch16<T, D, G>(p, max_e, s);
+  }
+}
+
 template <typename T, int D>
-int prefill_group(const PrefillParams& p, int num_reqs, int max_e, int group, hipStream_t s) {
+int prefill_group(const PrefillParams& p, int max_e, int group, hipStream_t s) {
   switch (group) {
-    case 1: return launch_prefill<T, D, 1>(p, num_reqs, max_e, s);
-    case 2: return launch_prefill<T, D, 2>(p, num_reqs, max_e, s);
-    case 4: return launch_prefill<T, D, 4>(p, num_reqs, max_e, s);
-    case 8: return launch_prefill<T, D, 8>(p, num_reqs, max_e, s);
-    case 16: return launch_prefill<T, D, 16>(p, num_reqs, max_e, s);
+    case 1: return launch_prefill<T, D, 1>(p, max_e, s);
+    case 2: return launch_prefill<T, D, 2>(p, max_e, s);
+    case 4: return launch_prefill<T, D, 4>(p, max_e, s);
+    case 8: return launch_prefill<T, D, 8>(p, max_e, s);
+    case 16: return launch_prefill<T, D, 16>(p, max_e, s);
     default:
       set_error("msgl_prefill_ragged: Hq/Hkv = %d not built (1, 2, 4, 8, 16)", group);
       return MSGL_ERR_UNSUPPORTED;
@@ -314,29 +812,56 @@ int prefill_group(const PrefillParams& p, int num_reqs, int max_e, int group, hi
 }
 
 template <typename T>
-int prefill_dim(const PrefillParams& p, int num_reqs, int max_e, int head_dim, int group, hipStream_t s) {
+int prefill_dim(const PrefillParams& p, int max_e, int head_dim, int group, hipStream_t s) {
   switch (head_dim) {
-    case 64: return prefill_group<T, 64>(p, num_reqs, max_e, group, s);
-    case 128: return prefill_group<T, 128>(p, num_reqs, max_e, group, s);
-    case 256: return prefill_group<T, 256>(p, num_reqs, max_e, group, s);
+    case 64: return prefill_group<T, 64>(p, max_e, group, s);
+    case 128: return prefill_group<T, 128>(p, max_e, group, s);
+    case 256: return prefill_group<T, 256>(p, max_e, group, s);
     default:
       set_error("msgl_prefill_ragged: head_dim %d not built (64, 128, 256)", head_dim);
       return MSGL_ERR_UNSUPPORTED;
   }
 }
 
+inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
 }  // namespace
 }  // namespace msgl
 
+extern "C" int32_t msgl_prefill_default_splits(int32_t num_reqs, int32_t num_qo_heads, int32_t num_kv_heads,
+                                               int32_t head_dim, int32_t max_extend_len, int32_t max_seq_len) {
+  using namespace msgl;
+  if (num_reqs <= 0 || num_kv_heads <= 0 || num_qo_heads < num_kv_heads || max_extend_len <= 0) return 1;
+  const int group = num_qo_heads / num_kv_heads;
+  const int bq = tokens_per_block16(head_dim, group) > 0 ? tokens_per_block16(head_dim, group) : 1;
+  const int64_t base = (int64_t)num_reqs * num_kv_heads * ((max_extend_len + bq - 1) / bq);
+  // about 8 resident workgroups' worth per CU of the 256-CU device
+  const int64_t target = 2048;
+  int64_t s = (target + base - 1) / base;
+  if (max_seq_len > 0) s = std::min<int64_t>(s, std::max<int64_t>(1, (max_seq_len + kMinChunk - 1) / kMinChunk));
+  s = std::max<int64_t>(1, std::min<int64_t>(s, kMaxSplits));
+  return (int32_t)s;
+}
+
+extern "C" int64_t msgl_prefill_workspace_size(int32_t num_tokens, int32_t num_qo_heads, int32_t head_dim,
+                                               int32_t max_splits) {
+  using namespace msgl;
+  if (max_splits <= 1 || num_tokens <= 0 || num_qo_heads <= 0 || head_dim <= 0) return 0;
+  const int64_t rows = (int64_t)max_splits * num_tokens * num_qo_heads;
+  return align256(rows * 8) + align256(rows * head_dim * 4);
+}
+
 extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, const int32_t* q_indptr,
                                    const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
-                                   int32_t num_reqs, int32_t max_extend_len, int32_t num_qo_heads,
+                                   int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                                   int32_t num_qo_heads,
                                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
-                                   int32_t dtype, float scale, void* out, void* stream) {
+                                   int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
   using namespace msgl;
   clear_error();
-  MSGL_CHECK_ARG(num_reqs >= 0 && max_extend_len >= 0, "msgl_prefill_ragged: sizes must be >= 0");
-  if (num_reqs == 0 || max_extend_len == 0) return MSGL_OK;
+  MSGL_CHECK_ARG(num_reqs >= 0 && num_tokens >= 0 && max_extend_len >= 0, "msgl_prefill_ragged: sizes must be >= 0");
+  if (num_reqs == 0 || max_extend_len == 0 || num_tokens == 0) return MSGL_OK;
   MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "msgl_prefill_ragged: sizes must be > 0");
   MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "msgl_prefill_ragged: Hq (%d) must be a multiple of Hkv (%d)",
                  num_qo_heads, num_kv_heads);
@@ -344,7 +869,9 @@ extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void
   MSGL_CHECK_ARG(page_size == 1 || seq_lens != nullptr, "msgl_prefill_ragged: page_size > 1 needs seq_lens");
   MSGL_CHECK_ARG(num_slots > 0 && num_slots <= ((int64_t)1 << 31) - 1,
                  "msgl_prefill_ragged: num_slots must be in [1, 2^31)");
-  MSGL_CHECK_ARG((int64_t)num_reqs * num_kv_heads <= 65535, "msgl_prefill_ragged: num_reqs * Hkv must be <= 65535");
+  MSGL_CHECK_ARG(scale > 0.f && scale < INFINITY, "msgl_prefill_ragged: scale must be positive and finite");
+  MSGL_CHECK_ARG(max_splits >= 1 && max_splits <= kMaxSplits, "msgl_prefill_ragged: max_splits must be in [1, %d]",
+                 kMaxSplits);
   MSGL_CHECK_ARG(q && k_pool && v_pool && q_indptr && kv_indptr && kv_indices && out,
                  "msgl_prefill_ragged: null pointer");
   MSGL_CHECK_ARG(((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) % 16 == 0,
@@ -362,17 +889,41 @@ extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void
   p.kv_indices = kv_indices;
   p.seq_lens = seq_lens;
   p.out = out;
+  p.part_o = nullptr;
+  p.part_ml = nullptr;
   p.num_slots = num_slots;
   p.hq = num_qo_heads;
   p.hkv = num_kv_heads;
   p.page_size = page_size;
+  p.num_reqs = num_reqs;
+  p.num_tokens = num_tokens;
+  p.splits = dtype == MSGL_F32 ? 1 : max_splits;  // fp32 runs one pass per block
+  p.chunk_len = 0;
+  if (p.splits > 1 && max_seq_len > 0) {
+    const int per = (max_seq_len + p.splits - 1) / p.splits;
+    p.chunk_len = std::max(kMinChunk, (per + KT - 1) / KT * KT);
+  }
+  p.nqb = 0;
+  p.items = 0;
   p.scale_log2 = scale * kLog2eP;
+  if (p.splits > 1) {
+    const int64_t need = msgl_prefill_workspace_size(num_tokens, num_qo_heads, head_dim, p.splits);
+    if (workspace == nullptr || workspace_bytes < need) {
+      set_error("msgl_prefill_ragged: workspace of %lld bytes needed for %d splits, got %lld", (long long)need,
+                p.splits, (long long)workspace_bytes);
+      return MSGL_ERR_WORKSPACE;
+    }
+    MSGL_CHECK_ARG((uintptr_t)workspace % 256 == 0, "msgl_prefill_ragged: workspace must be 256-byte aligned");
+    const int64_t rows = (int64_t)p.splits * num_tokens * num_qo_heads;
+    p.part_ml = reinterpret_cast<float2*>(workspace);
+    p.part_o = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + align256(rows * 8));
+  }
   const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
   switch (dtype) {
-    case MSGL_F32: return prefill_dim<float>(p, num_reqs, max_extend_len, head_dim, group, s);
-    case MSGL_BF16: return prefill_dim<bf16_t>(p, num_reqs, max_extend_len, head_dim, group, s);
-    case MSGL_F16: return prefill_dim<f16_t>(p, num_reqs, max_extend_len, head_dim, group, s);
+    case MSGL_F32: return prefill_dim<float>(p, max_extend_len, head_dim, group, s);
+    case MSGL_BF16: return prefill_dim<bf16_t>(p, max_extend_len, head_dim, group, s);
+    case MSGL_F16: return prefill_dim<f16_t>(p, max_extend_len, head_dim, group, s);
   }
   return MSGL_ERR_UNSUPPORTED;
 }

@@ -69,11 +69,14 @@ SIGNATURES = {
         [
             _c_p, _c_p, _c_p,  # q, k_pool, v_pool
             _c_p, _c_p, _c_p, _c_p,  # q_indptr, kv_indptr, kv_indices, seq_lens
-            _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,  # num_reqs, max_extend_len, Hq, Hkv, D
+            _c_i32, _c_i32, _c_i32, _c_i32,  # num_reqs, num_tokens, max_extend_len, max_seq_len
+            _c_i32, _c_i32, _c_i32,  # Hq, Hkv, D
             _c_i32, _c_i64, _c_i32, _c_f,  # page_size, num_slots, dtype, scale
-            _c_p, _c_p,  # out, stream
+            _c_i32, _c_p, _c_p, _c_i64, _c_p,  # max_splits, out, workspace, ws_bytes, stream
         ],
     ),
+    "msgl_prefill_default_splits": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
+    "msgl_prefill_workspace_size": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
 }
 
 _lib = None

@@ -52,6 +52,8 @@ class HipPrefillDevice:
     seq_lens: torch.Tensor  # [R]
     max_extend_len: int
     num_tokens: int
+    max_seq_len: int
+    max_splits: int
 
 
 class HipAttnBackend(BaseAttnBackend):
@@ -91,7 +93,11 @@ class HipAttnBackend(BaseAttnBackend):
 
     def _decode_workspace(self, batch_size: int, max_splits: int) -> Optional[torch.Tensor]:
         cfg = self.config
-        need = ops.decode_workspace_bytes(batch_size, cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, max_splits)
+        return self._shared_workspace(
+            ops.decode_workspace_bytes(batch_size, cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, max_splits)
+        )
+
+    def _shared_workspace(self, need: int) -> Optional[torch.Tensor]:
         if need == 0:
             return None
         if self._workspace is None or self._workspace.numel() < need:
@@ -138,7 +144,14 @@ class HipAttnBackend(BaseAttnBackend):
             seq_lens=_to_device(seq_lens, self.device),
             max_extend_len=int(max(extend_lens)),
             num_tokens=int(q_offsets[-1]),
+            max_seq_len=int(seq_lens.max()),
+            max_splits=1,
         )
+        cfg = self.config
+        if self.kv_cache.dtype != torch.float32:  # fp32 runs one pass per query block
+            dev.max_splits = ops.prefill_default_splits(
+                len(batch.reqs), cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, dev.max_extend_len, dev.max_seq_len
+            )
         return PrefillMetadata(
             last_indices=_to_device(np.array(q_offsets[1:], dtype=np.int32) - 1, self.device),
             q_offsets=q_offsets,
@@ -158,4 +171,9 @@ class HipAttnBackend(BaseAttnBackend):
             d.seq_lens,
             self.scale,
             max_extend_len=d.max_extend_len,
+            max_seq_len=d.max_seq_len,
+            max_splits=d.max_splits,
+            workspace=self._shared_workspace(
+                ops.prefill_workspace_bytes(d.num_tokens, self.config.num_qo_heads, self.config.head_dim, d.max_splits)
+            ),
         )

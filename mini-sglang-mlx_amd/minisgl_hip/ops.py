@@ -77,6 +77,25 @@ def decode_workspace(batch: int, num_qo_heads: int, num_kv_heads: int, head_dim:
     return torch.empty(need, dtype=torch.uint8, device=device)
 
 
+def prefill_default_splits(num_reqs: int, num_qo_heads: int, num_kv_heads: int, head_dim: int,
+                           max_extend_len: int, max_seq_len: int = 0) -> int:
+    return int(_lib.load().msgl_prefill_default_splits(num_reqs, num_qo_heads, num_kv_heads, head_dim,
+                                                       max_extend_len, max_seq_len))
+
+
+def prefill_workspace_bytes(num_tokens: int, num_qo_heads: int, head_dim: int, max_splits: int) -> int:
+    return int(_lib.load().msgl_prefill_workspace_size(num_tokens, num_qo_heads, head_dim, max_splits))
+
+
+def prefill_workspace(num_tokens: int, num_qo_heads: int, head_dim: int, max_splits: int,
+                      device) -> Optional[torch.Tensor]:
+    """A workspace for ``prefill_ragged_attention`` (None when no split)."""
+    need = prefill_workspace_bytes(num_tokens, num_qo_heads, head_dim, max_splits)
+    if need == 0:
+        return None
+    return torch.empty(need, dtype=torch.uint8, device=device)
+
+
 def paged_decode_attention(
     q: torch.Tensor,
     k_pool: torch.Tensor,
@@ -171,15 +190,21 @@ def prefill_ragged_attention(
     scale: Union[float, torch.Tensor],
     *,
     max_extend_len: int,
+    max_seq_len: int = 0,
     page_size: int = 1,
+    max_splits: Optional[int] = None,
     out: Optional[torch.Tensor] = None,
+    workspace: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Ragged prefill over cached prefixes; counterpart of attention/base.py:85-105.
 
     q [T, Hq, D] packed; request i owns q rows q_indptr[i]:q_indptr[i+1] and
     attends (bottom-right causal) to the first seq_lens[i] tokens of its KV at
     kv_indices[kv_indptr[i]:] (token slots, or page ids when page_size > 1).
-    ``max_extend_len`` must bound every request's extend length (host-known).
+    ``max_extend_len`` must bound every request's extend length (host-known);
+    ``max_seq_len`` (max total length, 0 = unknown) only tunes the key-range
+    split (its default and the chunk length). ``workspace`` (from ``prefill_workspace``) is allocated per
+    call when the split needs one and none large enough is given.
     """
     if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
         raise ValueError("q must be [T, Hq, D] and pools [N, Hkv, D]")
@@ -211,11 +236,17 @@ def prefill_ragged_attention(
     if t == 0:
         return out
     lib = _lib.load()
+    if max_splits is None:
+        max_splits = prefill_default_splits(num_reqs, hq, hkv, d, int(max_extend_len), int(max_seq_len))
+    need = prefill_workspace_bytes(t, hq, d, max_splits) if q.dtype != torch.float32 else 0
+    if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     status = lib.msgl_prefill_ragged(
         _lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool),
         _lib.ptr(q_indptr), _lib.ptr(kv_indptr), _lib.ptr(kv_indices), _lib.ptr(seq_lens),
-        num_reqs, int(max_extend_len), hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
-        _lib.ptr(out), _lib.current_stream(dev),
+        num_reqs, t, int(max_extend_len), int(max_seq_len), hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
+        int(max_splits), _lib.ptr(out), _lib.ptr(workspace), ws_bytes, _lib.current_stream(dev),
     )
     _lib.check(status, "msgl_prefill_ragged")
     return out

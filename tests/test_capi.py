@@ -49,6 +49,20 @@ def test_abi_version_and_sizes():
     assert lib.msgl_paged_decode_default_splits(1, 8, 100) == 2  # capped by ceil(100 / 64)
 
 
+def test_prefill_sizes():
+    lib = _lib.load()
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    assert lib.msgl_prefill_workspace_size(2048, 16, 128, 1) == 0
+    rows = 4 * 2048 * 16
+    assert lib.msgl_prefill_workspace_size(2048, 16, 128, 4) == up(rows * 8) + up(rows * 128 * 4)
+    # 16 requests x 8 kv heads x ceil(512 / 64) blocks = 1024 workgroups: two chunks reach 2048
+    assert lib.msgl_prefill_default_splits(16, 16, 8, 128, 512, 4096) == 2
+    assert lib.msgl_prefill_default_splits(16, 16, 8, 128, 199, 4160) == 4
+    assert lib.msgl_prefill_default_splits(1, 32, 8, 128, 64, 100000) == 16  # capped at 16
+    assert lib.msgl_prefill_default_splits(1, 32, 8, 128, 64, 300) == 2  # >= 256 keys per chunk
+    assert lib.msgl_prefill_default_splits(0, 32, 8, 128, 64, 300) == 1
+
+
 def test_host_side_argument_errors():
     lib = _lib.load()
     nul = None
@@ -67,6 +81,19 @@ def test_host_side_argument_errors():
     # unsupported head_dim is reported (dispatch happens before any launch)
     st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 1, 16, 8, 96, 1, 100, 1, 0.1, 1, 16, nul, 0, nul)
     assert st == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
+    # prefill: (q, kp, vp, q_indptr, kv_indptr, kv_indices, seq_lens, R, T, maxE, maxL, Hq, Hkv, D, page, slots,
+    #           dtype, scale, splits, out, ws, ws_bytes, stream)
+    pf = lambda splits, ws_bytes, dtype=1, d=128, scale=0.1: lib.msgl_prefill_ragged(  # noqa: E731
+        16, 16, 16, 16, 16, 16, nul, 2, 64, 32, 0, 16, 8, d, 1, 100, dtype, scale, splits, 16, 256, ws_bytes, nul)
+    assert pf(1, 0, scale=0.0) == _lib.MSGL_ERR_INVALID and "scale" in _lib.last_error()
+    assert pf(1, 0, scale=-0.1) == _lib.MSGL_ERR_INVALID
+    assert pf(0, 0) == _lib.MSGL_ERR_INVALID and "max_splits" in _lib.last_error()
+    assert pf(17, 0) == _lib.MSGL_ERR_INVALID
+    assert pf(4, 0) == _lib.MSGL_ERR_WORKSPACE
+    assert pf(4, 1 << 30, d=96) == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
+    assert pf(4, 0, dtype=0, d=96) == _lib.MSGL_ERR_UNSUPPORTED  # fp32 ignores splits: no workspace needed
+    assert lib.msgl_prefill_ragged(nul, nul, nul, nul, nul, nul, nul, 0, 0, 0, 0, 16, 8, 128, 1, 100, 1, 0.1, 1,
+                                   nul, nul, 0, nul) == _lib.MSGL_OK
     # store_kv: zero tokens is a no-op; bad row size is unsupported
     assert lib.msgl_store_kv(nul, nul, nul, nul, nul, 0, 8, 128, 10, 1, nul) == _lib.MSGL_OK
     assert lib.msgl_store_kv(16, 16, 16, 16, 16, 4, 1, 3, 10, 1, nul) == _lib.MSGL_ERR_UNSUPPORTED

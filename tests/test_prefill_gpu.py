@@ -94,3 +94,39 @@ def test_prefill_cfg4_sampled(cuda_device):
     )
     torch.cuda.synchronize()
     assert torch.equal(out, out2), "prefill is not deterministic"
+
+
+@pytest.mark.parametrize("dtype", ["bf16", "f16"])
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (32, 8)])
+@pytest.mark.parametrize("splits", [1, 2, 5, 16])
+def test_prefill_key_splits(cuda_device, hq, hkv, dtype, splits):
+    """Long prefixes cut into 1..16 key chunks (merged in fp32), one chunk longer
+    than the 1024-key slot window (splits=1), rows that see no key of a chunk."""
+    dt = DTYPES[dtype]
+    case = workloads.prefill_case_from_lens([0, 1500, 2500, 700, 33], [300, 64, 129, 1, 200], num_slots=16384,
+                                            seed=5)
+    print(f"case prefill splits={splits} {hq}/{hkv} {dtype}", flush=True)
+    n = case.num_slots
+    kp = randn((n, hkv, 128), 40, dt).to(cuda_device)
+    vp = randn((n, hkv, 128), 41, dt).to(cuda_device)
+    q = randn((case.num_tokens, hq, 128), 42, dt).to(cuda_device)
+    kn = randn((case.num_tokens, hkv, 128), 43, dt).to(cuda_device)
+    vn = randn((case.num_tokens, hkv, 128), 44, dt).to(cuda_device)
+    ops.store_kv(kn, vn, i32(case.out_loc, cuda_device), kp, vp)
+    out = ops.prefill_ragged_attention(
+        q, kp, vp, i32(case.q_indptr, cuda_device), i32(case.kv_indptr, cuda_device),
+        i32(case.kv_indices, cuda_device), None, 128**-0.5, max_extend_len=int(case.extend_lens.max()),
+        max_splits=splits,
+    )
+    torch.cuda.synchronize()
+    ref = _oracle(case, q, kn, vn, kp, vp, 128)
+    assert_close(out, ref, dt, f"prefill splits={splits} {hq}/{hkv} {dtype}")
+
+
+def test_prefill_splits_page16(cuda_device):
+    case = workloads.prefill_case_from_lens([0, 15, 1600, 40, 2333], [5, 1, 33, 100, 64], num_slots=16384,
+                                            page_size=16, seed=6)
+    print("case prefill splits page16", flush=True)
+    q, kn, vn, kp, vp, out = _run(case, 32, 8, 128, torch.bfloat16, cuda_device, 50, page_size=16)
+    ref = _oracle(case, q, kn, vn, kp, vp, 128)
+    assert_close(out, ref, torch.bfloat16, "prefill splits page16")
