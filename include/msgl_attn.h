@@ -16,6 +16,9 @@
  *   msgl_paged_decode_store  kvcache/pool.py:47-50 + attention/metal.py:112-131 in one launch
  *   msgl_prefill_ragged      attention/base.py:85-105     BaseAttnBackend._forward_prefill
  *                            (+ _default_splits, _workspace_size)
+ *   msgl_build_step_indices  scheduler/scheduler.py:154-157 + attention/metal.py:145-152
+ *                            + attention/base.py:70-83 (index metadata, on the GPU)
+ *   msgl_table_scatter       device mirror of scheduler/cache.py:53-72's page-table writes
  *
  * Layouts (identical to the reference, no transposes at the boundary):
  *   q, out   [T, Hq, D]   row-major, dtype `dtype`
@@ -166,6 +169,35 @@ int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, c
                         int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                         int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Per-step index construction on the GPU from a device copy of the page table
+ * req_to_token [num_rows, row_stride] (token-granular slots, as the
+ * scheduler's page_table, engine/engine.py:74). Per request r (device int32
+ * arrays of num_reqs): row table_idx[r], tokens [cached_len[r], device_len[r])
+ * are this step's. Writes, bit-exact with:
+ *   q_indptr [R+1], last_indices [R]   attention/base.py:70-83 (q_offsets, last_indices)
+ *   positions, out_loc [T]             scheduler/scheduler.py:154-157
+ *   kv_indptr [R+1], kv_indices        attention/metal.py:145-152 (token slots of
+ *                                      [0, device_len)); with page_size > 1 page
+ *                                      ids of ceil(device_len / page_size) pages
+ * T = q_indptr[R] and kv_indptr[R] are left on the device; outputs stop at
+ * token_capacity / kv_capacity. positions, out_loc and last_indices may be
+ * NULL. Table entries outside the table read as -1. Two launches.
+ */
+int msgl_build_step_indices(const int32_t* req_to_token, int64_t num_rows, int64_t row_stride,
+                            const int32_t* table_idx, const int32_t* cached_len, const int32_t* device_len,
+                            int32_t num_reqs, int32_t page_size, int32_t* q_indptr, int32_t* positions,
+                            int32_t* out_loc, int32_t* last_indices, int64_t token_capacity, int32_t* kv_indptr,
+                            int32_t* kv_indices, int64_t kv_capacity, void* stream);
+
+/*
+ * req_to_token[rows[i], cols[i]] = values[i] for i < n (entries outside the
+ * table are skipped): keeps the device copy of the page table in step with the
+ * slots the scheduler allocates on the host (scheduler/cache.py:53-72).
+ */
+int msgl_table_scatter(int32_t* req_to_token, int64_t num_rows, int64_t row_stride, const int32_t* rows,
+                       const int32_t* cols, const int32_t* values, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

@@ -75,6 +75,16 @@ SIGNATURES = {
             _c_i32, _c_p, _c_p, _c_i64, _c_p,  # max_splits, out, workspace, ws_bytes, stream
         ],
     ),
+    "msgl_build_step_indices": (
+        ctypes.c_int,
+        [
+            _c_p, _c_i64, _c_i64,  # req_to_token, num_rows, row_stride
+            _c_p, _c_p, _c_p, _c_i32, _c_i32,  # table_idx, cached_len, device_len, num_reqs, page_size
+            _c_p, _c_p, _c_p, _c_p, _c_i64,  # q_indptr, positions, out_loc, last_indices, token_capacity
+            _c_p, _c_p, _c_i64, _c_p,  # kv_indptr, kv_indices, kv_capacity, stream
+        ],
+    ),
+    "msgl_table_scatter": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p]),
     "msgl_prefill_default_splits": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "msgl_prefill_workspace_size": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
 }

@@ -250,3 +250,72 @@ def prefill_ragged_attention(
     )
     _lib.check(status, "msgl_prefill_ragged")
     return out
+
+
+def build_step_indices(
+    req_to_token: torch.Tensor,
+    table_idx: torch.Tensor,
+    cached_len: torch.Tensor,
+    device_len: torch.Tensor,
+    *,
+    num_tokens: int,
+    num_kv: int,
+    page_size: int = 1,
+) -> dict:
+    """Step metadata built on the GPU from a device page table.
+
+    Counterpart of scheduler/scheduler.py:154-157 (positions, out_loc),
+    attention/base.py:70-83 (q_indptr = q_offsets, last_indices) and
+    attention/metal.py:145-152 (kv_indptr, kv_indices; page ids of
+    ceil(L / page_size) pages when page_size > 1). ``num_tokens`` =
+    sum(device_len - cached_len) and ``num_kv`` = sum of (page-)lengths are
+    host-known sizes of the outputs. Returns device int32 tensors.
+    """
+    if req_to_token.dim() != 2:
+        raise ValueError("req_to_token must be [rows, max_seq_len]")
+    r = table_idx.shape[0]
+    if cached_len.shape != (r,) or device_len.shape != (r,):
+        raise ValueError("table_idx, cached_len and device_len must all be [R]")
+    dev = req_to_token.device
+    for name, t in (("req_to_token", req_to_token), ("table_idx", table_idx), ("cached_len", cached_len),
+                    ("device_len", device_len)):
+        _check_index(name, t, dev)
+    i32 = dict(dtype=torch.int32, device=dev)
+    out = {
+        "q_indptr": torch.empty(r + 1, **i32),
+        "positions": torch.empty(num_tokens, **i32),
+        "out_loc": torch.empty(num_tokens, **i32),
+        "last_indices": torch.empty(r, **i32),
+        "kv_indptr": torch.empty(r + 1, **i32),
+        "kv_indices": torch.empty(num_kv, **i32),
+    }
+    if r == 0:
+        out["q_indptr"].zero_()
+        out["kv_indptr"].zero_()
+        return out
+    status = _lib.load().msgl_build_step_indices(
+        _lib.ptr(req_to_token), req_to_token.shape[0], req_to_token.shape[1],
+        _lib.ptr(table_idx), _lib.ptr(cached_len), _lib.ptr(device_len), r, page_size,
+        _lib.ptr(out["q_indptr"]), _lib.ptr(out["positions"]), _lib.ptr(out["out_loc"]),
+        _lib.ptr(out["last_indices"]), num_tokens,
+        _lib.ptr(out["kv_indptr"]), _lib.ptr(out["kv_indices"]), num_kv, _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_build_step_indices")
+    return out
+
+
+def table_scatter(req_to_token: torch.Tensor, rows: torch.Tensor, cols: torch.Tensor, values: torch.Tensor) -> None:
+    """req_to_token[rows, cols] = values on the device (entries outside the table skipped)."""
+    n = rows.shape[0]
+    if cols.shape != (n,) or values.shape != (n,) or req_to_token.dim() != 2:
+        raise ValueError("rows, cols and values must be [n]; req_to_token [rows, max_seq_len]")
+    dev = req_to_token.device
+    for name, t in (("req_to_token", req_to_token), ("rows", rows), ("cols", cols), ("values", values)):
+        _check_index(name, t, dev)
+    if n == 0:
+        return
+    status = _lib.load().msgl_table_scatter(
+        _lib.ptr(req_to_token), req_to_token.shape[0], req_to_token.shape[1], _lib.ptr(rows), _lib.ptr(cols),
+        _lib.ptr(values), n, _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_table_scatter")

@@ -94,6 +94,18 @@ def test_host_side_argument_errors():
     assert pf(4, 0, dtype=0, d=96) == _lib.MSGL_ERR_UNSUPPORTED  # fp32 ignores splits: no workspace needed
     assert lib.msgl_prefill_ragged(nul, nul, nul, nul, nul, nul, nul, 0, 0, 0, 0, 16, 8, 128, 1, 100, 1, 0.1, 1,
                                    nul, nul, 0, nul) == _lib.MSGL_OK
+    # step indices: (table, rows, stride, table_idx, cached, device_len, R, page, q_indptr, positions, out_loc,
+    #                last, token_cap, kv_indptr, kv_indices, kv_cap, stream)
+    bi = lambda R, page=1, rows_=4, stride=64, tok_out=16, kv_out=16: lib.msgl_build_step_indices(  # noqa: E731
+        16, rows_, stride, 16, 16, 16, R, page, 16, tok_out, nul, nul, 8, 16, kv_out, 8, nul)
+    assert bi(0) == _lib.MSGL_OK
+    assert bi(-1) == _lib.MSGL_ERR_INVALID
+    assert bi(2, page=0) == _lib.MSGL_ERR_INVALID and "page_size" in _lib.last_error()
+    assert bi(2, rows_=0) == _lib.MSGL_ERR_INVALID
+    assert bi(2, tok_out=nul) == _lib.MSGL_ERR_INVALID and "null" in _lib.last_error()
+    assert bi(2, kv_out=nul) == _lib.MSGL_ERR_INVALID
+    assert lib.msgl_table_scatter(nul, 4, 64, nul, nul, nul, 0, nul) == _lib.MSGL_OK
+    assert lib.msgl_table_scatter(16, 4, 64, nul, 16, 16, 3, nul) == _lib.MSGL_ERR_INVALID
     # store_kv: zero tokens is a no-op; bad row size is unsupported
     assert lib.msgl_store_kv(nul, nul, nul, nul, nul, 0, 8, 128, 10, 1, nul) == _lib.MSGL_OK
     assert lib.msgl_store_kv(16, 16, 16, 16, 16, 4, 1, 3, 10, 1, nul) == _lib.MSGL_ERR_UNSUPPORTED
