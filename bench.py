@@ -1,10 +1,11 @@
-"""Benchmark: paged decode attention on one MI355X (the attention hot path).
+"""Benchmark: the attention hot path on one MI355X.
 
-One step = one decode step of Qwen3-0.6B attention over all 28 layers for a
-batch of 128 requests with ragged contexts U[200, 2048] (seed 0), page size 1,
-a 262144-slot bf16 KV pool per layer with randomly permuted slots: per layer,
-the new token's K/V rows are scattered into their slots (KV store) and paged
-decode attention runs over the pool. Inputs are resident in HBM before timing.
+Default workload (``--workload decode``): one step = one decode step of
+Qwen3-0.6B attention over all 28 layers for a batch of 128 requests with
+ragged contexts U[200, 2048] (seed 0), page size 1, a 262144-slot bf16 KV pool
+per layer with randomly permuted slots: per layer, the new token's K/V rows
+are scattered into their slots (KV store) and paged decode attention runs over
+the pool. Inputs are resident in HBM before timing.
 
 Prints one JSON line. ``value`` is algorithmic GB/s over the whole step
 (decode bytes = ΣL·Hkv·D·2·2 + B·Hq·D·2·2 + ΣL·4 + (B+1)·4 per layer, plus the
@@ -13,6 +14,16 @@ paged-decode kernel with the KV store fused in, plus its split-K merge kernel
 -- timed with HIP events around one layer per step (rotating through the
 layers) inside the timed region, on the launch stream;
 ``cpu_baseline`` times the CPU restatement of the reference's naive backend.
+
+Other workloads (one JSON line each, same fields):
+  decode8b  paged decode, Qwen3-8B heads (32 q / 8 kv / 128), batch 256,
+            context U[1024, 8192], page 16, 4M-slot pool (one layer)
+  prefill   ragged chunked prefill, Qwen3-0.6B heads, 16 requests, prefix
+            U[0, 4096], extend U[64, 512] rescaled to <= 2048 packed tokens,
+            rotating over 28 layers' pools
+  mixed     one continuous-batching step, Qwen3-8B heads, page 16, 8M-slot pool:
+            128 decode requests (context U[512, 32768]) + chunks of 1024 over
+            prefixes 0 and 8192, indices built on the GPU from the page table
 """
 
 import argparse
@@ -39,6 +50,7 @@ TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_cfg2_traffic.txt"
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "prefill", "mixed"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
@@ -49,11 +61,11 @@ def parse_args():
     return ap.parse_args()
 
 
-def read_traffic():
-    """HBM bytes per decode launch measured with rocprofv3 counters (see the file), or None."""
-    if not TRAFFIC_FILE.exists():
+def read_traffic(path):
+    """HBM bytes per launch measured with rocprofv3 counters (see the file), or None."""
+    if not path.exists():
         return None
-    for line in TRAFFIC_FILE.read_text().splitlines():
+    for line in path.read_text().splitlines():
         if line.startswith("traffic_bytes_per_launch:"):
             return float(line.split(":", 1)[1].strip())
     return None
@@ -115,8 +127,6 @@ def main():
 
     import torch
 
-    from minisgl_hip import ops, workloads
-
     dev = torch.device("cuda:0")
     if args.copy_calibration:
         src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
@@ -125,6 +135,18 @@ def main():
             dst.copy_(src)
         torch.cuda.synchronize()
         del src, dst
+    if args.workload != "decode":
+        line = {"decode8b": bench_decode8b, "prefill": bench_prefill, "mixed": bench_mixed}[args.workload](args, dev)
+        print(json.dumps(line), flush=True)
+        return
+    bench_decode(args, dev)
+
+
+def bench_decode(args, dev):
+    import torch
+
+    from minisgl_hip import ops, workloads
+
     c = workloads.decode_case(BATCH, LO, HI, POOL, 1, seed=0)
     dec_bytes = workloads.decode_bytes(c.lens, HQ, HKV, D, 2)
     store_bytes = BATCH * HKV * D * 2 * 2 * 2  # K and V rows, read + written
@@ -176,7 +198,7 @@ def main():
     ms_per_step = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9
     achieved = (dec_bytes + store_bytes) / dec_avg_s / 1e9  # one layer's decode+store launch + merge
-    traffic = read_traffic()
+    traffic = read_traffic(TRAFFIC_FILE)
 
     cpu = None
     if not args.no_cpu:
@@ -236,6 +258,200 @@ def main():
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def _timed(args, run, timed_call=None):
+    """Warm up, then time ``args.steps`` calls of run(i); ``timed_call`` (if given) is
+    bracketed by HIP events on the launch stream inside each step. Returns
+    (seconds per step, event seconds per step or None)."""
+    import torch
+
+    for i in range(args.warmup):
+        run(i, None)
+    torch.cuda.synchronize()
+    ev = [[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in range(args.steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        run(i, ev[i])
+    torch.cuda.synchronize()
+    elapsed = (time.perf_counter() - t0) / args.steps
+    ev_s = float(np.mean([a.elapsed_time(b) for a, b in ev])) / 1e3
+    return elapsed, ev_s
+
+
+def _line(args, metric, value, unit, ms_per_step, workload, extra, roofline, higher=True):
+    line = {
+        "metric": metric,
+        "value": round(value, 3),
+        "unit": unit,
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": higher,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": workload, **extra},
+        "roofline": roofline,
+        "cpu_baseline": None,
+    }
+    return line
+
+
+def bench_decode8b(args, dev):
+    """Paged decode, Qwen3-8B heads, batch 256, L ~ U[1024, 8192], page 16, 4M-slot pool; one layer."""
+    import torch
+
+    from minisgl_hip import ops, workloads
+
+    hq, hkv, d, batch, pool, ps = 32, 8, 128, 256, 4 << 20, 16
+    c = workloads.decode_case(batch, 1024, 8192, pool, ps, seed=0)
+    nbytes = workloads.decode_bytes(c.lens, hq, hkv, d, 2, ps)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    kp = torch.randn((pool, hkv, d), generator=gen, device=dev, dtype=torch.bfloat16)
+    vp = torch.randn((pool, hkv, d), generator=gen, device=dev, dtype=torch.bfloat16)
+    q = torch.randn((batch, hq, d), generator=gen, device=dev, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    pi = torch.from_numpy(c.page_indptr).to(dev)
+    pid = torch.from_numpy(c.page_ids).to(dev)
+    sl = torch.from_numpy(c.lens).to(dev)
+    splits = args.splits or ops.default_splits(batch, hkv, int(c.lens.max()))
+    ws = ops.decode_workspace(batch, hq, hkv, d, splits, dev)
+
+    def run(i, ev):
+        if ev:
+            ev[0].record()
+        ops.paged_decode_attention(q, kp, vp, pi, pid, d**-0.5, seq_lens=sl, page_size=ps, max_splits=splits,
+                                   out=out, workspace=ws)
+        if ev:
+            ev[1].record()
+
+    sec, ev_s = _timed(args, run)
+    gbs = nbytes / sec / 1e9
+    ach = nbytes / ev_s / 1e9
+    return _line(
+        args, "paged-decode HBM GB/s, batch 256, Qwen3-8B heads, page 16", gbs, "GB/s", sec * 1e3,
+        "paged decode, Qwen3-8B attention (32 q / 8 kv heads, head_dim 128), one layer; batch 256, context "
+        "U[1024,8192] (seed 0), page_size 16, 4M-slot bf16 pool, random pages; split-K + merge",
+        {"batch": batch, "sum_context": int(c.lens.sum()), "max_splits": splits, "bytes_per_step": nbytes,
+         "us_per_layer": round(sec * 1e6, 2)},
+        {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": read_traffic(ROOT / "profiles" / "paged_decode_cfg3_traffic.txt")},
+    )
+
+
+MFMA_PEAK_TFLOPS = 2500.0
+
+
+def bench_prefill(args, dev):
+    """Ragged prefill, 16 requests over cached prefixes, Qwen3-0.6B heads; 28 layers' pools in rotation."""
+    import torch
+
+    from minisgl_hip import ops, workloads
+
+    pool = 1 << 17
+    case = workloads.prefill_case(16, 4096, 64, 512, 2048, num_slots=pool, seed=0)
+    flops, nbytes = workloads.prefill_flops_bytes(case.prefix_lens, case.extend_lens, HQ, HKV, D, 2)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    kps = [torch.randn((pool, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    vps = [torch.randn((pool, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    t = case.num_tokens
+    q = torch.randn((t, HQ, D), generator=gen, device=dev, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+    qi = torch.from_numpy(case.q_indptr).to(dev)
+    ki = torch.from_numpy(case.kv_indptr).to(dev)
+    kx = torch.from_numpy(case.kv_indices).to(dev)
+    maxe, maxs = int(case.extend_lens.max()), int(case.seq_lens.max())
+    splits = args.splits or ops.prefill_default_splits(16, HQ, HKV, D, maxe, maxs)
+    ws = ops.prefill_workspace(16, t, maxe, HQ, HKV, D, splits, dev)
+
+    def run(i, ev):
+        layer = i % LAYERS
+        if ev:
+            ev[0].record()
+        ops.prefill_ragged_attention(q, kps[layer], vps[layer], qi, ki, kx, None, D**-0.5, max_extend_len=maxe,
+                                     max_seq_len=maxs, max_splits=splits, out=out, workspace=ws)
+        if ev:
+            ev[1].record()
+
+    sec, ev_s = _timed(args, run)
+    tflops = flops / ev_s / 1e12
+    gbs = nbytes / ev_s / 1e9
+    return _line(
+        args, "ragged-prefill attention µs/layer, 16 requests over cached prefixes, Qwen3-0.6B heads",
+        sec * 1e6, "us", sec * 1e3,
+        "ragged chunked prefill, Qwen3-0.6B attention (16 q / 8 kv heads, head_dim 128); 16 requests, prefix "
+        "U[0,4096], extend U[64,512] rescaled to <= 2048 packed tokens (seed 0), page_size 1, 131072-slot "
+        "bf16 pools of 28 layers in rotation; bottom-right causal",
+        {"requests": 16, "packed_tokens": t, "sum_prefix": int(case.prefix_lens.sum()), "max_splits": splits,
+         "flops_per_step": flops, "bytes_per_step": nbytes, "tflops": round(tflops, 2),
+         "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4)},
+        {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(ROOT / "profiles" / "prefill_cfg4_traffic.txt")},
+        higher=False,
+    )
+
+
+def bench_mixed(args, dev):
+    """One mixed step (GPU index build + stores + decode + prefill), Qwen3-8B heads, page 16."""
+    import torch
+
+    from minisgl_hip import workloads
+    from minisgl_hip.mixed import MixedStep
+
+    hq, hkv, d, pool, ps = 32, 8, 128, 8 << 20, 16
+    case = workloads.mixed_case(128, 512, 32768, [0, 8192], 1024, num_slots=pool, page_size=ps, seed=0)
+    nd = case.num_decode
+    dec_lens = case.device_len[:nd]
+    dec_bytes = workloads.decode_bytes(dec_lens, hq, hkv, d, 2, ps)
+    pre = slice(nd, case.num_reqs)
+    ext = case.device_len[pre] - case.cached_len[pre]
+    pf_flops, pf_bytes = workloads.prefill_flops_bytes(case.cached_len[pre], ext, hq, hkv, d, 2)
+    store_bytes = case.num_tokens * hkv * d * 2 * 2 * 2
+    nbytes = dec_bytes + pf_bytes + store_bytes
+    gen = torch.Generator(device=dev).manual_seed(0)
+    kp = torch.randn((pool, hkv, d), generator=gen, device=dev, dtype=torch.bfloat16)
+    vp = torch.randn((pool, hkv, d), generator=gen, device=dev, dtype=torch.bfloat16)
+    t = case.num_tokens
+    q = torch.randn((t, hq, d), generator=gen, device=dev, dtype=torch.bfloat16)
+    kn = torch.randn((t, hkv, d), generator=gen, device=dev, dtype=torch.bfloat16)
+    vn = torch.randn((t, hkv, d), generator=gen, device=dev, dtype=torch.bfloat16)
+    out = torch.empty_like(q)
+
+    def i32(x):
+        return torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(dev)
+
+    step = MixedStep(i32(case.req_to_token), i32(case.table_idx), i32(case.cached_len), i32(case.device_len),
+                     num_decode=nd, num_tokens=t, num_pages=case.num_pages, max_chunk=case.max_chunk,
+                     max_seq_len=int(case.device_len.max()), num_qo_heads=hq, num_kv_heads=hkv, head_dim=d,
+                     page_size=ps, decode_splits=args.splits or None)
+
+    def run(i, ev):
+        if ev:
+            ev[0].record()
+        step.run(q, kn, vn, kp, vp, out, d**-0.5)
+        if ev:
+            ev[1].record()
+
+    sec, ev_s = _timed(args, run)
+    ach = nbytes / ev_s / 1e9
+    return _line(
+        args, "mixed continuous-batching step µs (decode + prefill + GPU index build), Qwen3-8B heads, page 16",
+        sec * 1e6, "us", sec * 1e3,
+        "one step, Qwen3-8B attention (32 q / 8 kv heads, head_dim 128), one layer, page_size 16, 8M-slot bf16 "
+        "pool: 128 decode requests (context U[512,32768], seed 0) + 2 prefill chunks of 1024 over prefixes "
+        "0 and 8192; indices built on the GPU from a req_to_token table",
+        {"decode_requests": nd, "decode_sum_context": int(dec_lens.sum()), "prefill_tokens": int(ext.sum()),
+         "decode_bytes": dec_bytes, "prefill_flops": pf_flops, "prefill_bytes": pf_bytes,
+         "store_bytes": store_bytes, "decode_splits": step.decode_splits, "prefill_splits": step.prefill_splits,
+         "step_gbs": round(nbytes / sec / 1e9, 2)},
+        {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None},
+        higher=False,
+    )
 
 
 if __name__ == "__main__":

@@ -132,9 +132,12 @@ int msgl_paged_decode_store(const void* q, const void* k_new, const void* v_new,
 int32_t msgl_prefill_default_splits(int32_t num_reqs, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                                     int32_t max_extend_len, int32_t max_seq_len);
 
-/* Bytes of workspace msgl_prefill_ragged needs for max_splits (0 when
- * max_splits <= 1): fp32 (m, l) and unnormalised O per chunk and query row. */
-int64_t msgl_prefill_workspace_size(int32_t num_tokens, int32_t num_qo_heads, int32_t head_dim, int32_t max_splits);
+/* Bytes of workspace msgl_prefill_ragged needs for bf16/fp16 (fp32 needs
+ * none): the work list of (request, query block, chunk, kv head) items, and
+ * with max_splits > 1 the fp32 (m, l) and unnormalised O per chunk and query
+ * row. 0 for invalid sizes. */
+int64_t msgl_prefill_workspace_size(int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
+                                    int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t max_splits);
 
 /*
  * Ragged chunked-prefill attention over a paged pool, one launch per batch.
@@ -156,9 +159,10 @@ int64_t msgl_prefill_workspace_size(int32_t num_tokens, int32_t num_qo_heads, in
  *              block is cut evenly. Only the speed depends on it.
  *   scale      softmax scale, > 0 (attention/base.py:45: head_dim^-0.5)
  *   max_splits chunks per query block's key range, 1..16 (bf16/fp16; fp32
- *              always runs one pass); > 1 needs
- *              msgl_prefill_workspace_size(num_tokens, Hq, D, max_splits) bytes
- *              of 256-byte aligned workspace
+ *              always runs one pass)
+ *   workspace  bf16/fp16: msgl_prefill_workspace_size(num_reqs, num_tokens,
+ *              max_extend_len, Hq, Hkv, D, max_splits) bytes, 256-byte aligned
+ *              (fp32: may be NULL). Consecutive calls on one stream may share it.
  *   out        [T, Hq, D]
  * Query t of request i sees keys j <= P_i + t (MLX's bottom-right causal
  * mask, docs/04-attention.md:35-36); E_i <= L_i is required.

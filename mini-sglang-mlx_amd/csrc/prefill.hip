@@ -12,8 +12,8 @@
 // of one (request, kv head) and one contiguous range of that block's keys.
 //
 // bf16 / fp16 (prefill16_kernel), the serving path:
-//  * 4 wavefronts x 32 query rows (16 for head_dim 256): two 16-row MFMA
-//    column blocks per wavefront share every K fragment and every V operand.
+//  * 4 wavefronts x 32 query rows, all products on v_mfma_f32_32x32x16 (the
+//    16x16x32 form runs at half its rate on gfx950).
 //  * 32-key K and V tiles are gathered from the pool straight into LDS with
 //    gfx950's global_load_lds_dwordx4 (16 bytes per lane, no register
 //    staging) into a ring of NS stages, NS-1 tiles ahead of the compute. The
@@ -24,11 +24,12 @@
 //    (chunk c of row r lives at c ^ swz(r)); the K operand reads (16 rows,
 //    same chunk) and the transposing V reads (4 rows x 2 chunks per 16 lanes)
 //    are bank-conflict free on the 64-bank LDS.
-//  * S^T = K Q^T with v_mfma_f32_16x16x32_{bf16,f16}: lane (query col l%16,
-//    key group l/16) holds 4 keys of each 16-key tile, which is exactly the A
-//    operand layout P needs for O += P V (converted in registers, no shuffle).
-//    The B operand of P V (keys contiguous per lane) is read from the
-//    row-major V tile with ds_read_b64_tr_b16.
+//  * S^T = K Q^T per 32-key tile: lane l holds 16 keys (8c + 4(l/32) + r) of
+//    query row l%32, which are exactly the A operand slots P needs for the two
+//    16-key steps of O += P V (converted in registers, no shuffle); a row's max
+//    and sum take one exchange with lane l^32. The B operand of P V (keys
+//    contiguous per lane) is read from the row-major V tile with
+//    ds_read_b64_tr_b16.
 //  * Online softmax per query row in the exp2 domain, scores scaled inside
 //    the exponent's FMA.
 //  * Split-K: a block's visible key range [0, kv_end) is cut into at most
@@ -38,16 +39,17 @@
 //    directly; otherwise each chunk writes (m, l, unnormalised O) in fp32 to
 //    the workspace and prefill_merge_kernel combines them.
 //  * Online softmax with a lazily moved reference maximum (see the loop).
-//  * Workgroups are ordered (kv head, request, chunk, block) and remapped
-//    over the 8 XCDs (hardware dispatches workgroup i to XCD i % 8) so that
-//    each XCD takes a contiguous range: the blocks sharing a K/V chunk share
-//    one L2, and with 8 kv heads each XCD serves one head.
+//  * A one-workgroup plan kernel lists the (request, query block, chunk)
+//    items that have keys, longest first, each expanded to the kv heads; the
+//    attention grid reads its item from the list, so no empty workgroup sits
+//    between real ones and the dispatcher hands out long items first.
 //
 // fp32 (prefill_f32_kernel): one pass per block, 4 wavefronts x 16 rows,
 // register-staged gather into padded LDS tiles, v_mfma_f32_16x16x4f32.
 //
 // Causal tiles past a block's last visible key are never loaded.
 #include <algorithm>
+#include <type_traits>
 
 #include "msgl_common.h"
 
@@ -71,15 +73,18 @@ struct PrefillParams {
   const int32_t* kv_indices;
   const int32_t* seq_lens;
   void* out;
-  float* part_o;    // [splits][num_tokens][hq][D]
-  float2* part_ml;  // [splits][num_tokens][hq]
+  float* part_o;     // [splits][num_tokens][hq][D]
+  float2* part_ml;   // [splits][num_tokens][hq]
+  int4* plan;        // work list: (request, kv head, query block, chunk), longest first
+  int* plan_count;   // its length
   int64_t num_slots;
   int hq, hkv, page_size;
   int num_reqs, num_tokens;
   int splits;     // key chunks per block (grid dimension)
   int chunk_len;  // keys per chunk, 0 = per block
   int nqb;      // query blocks per request (grid dimension)
-  int items;    // workgroups with a logical index
+  int items;    // (request, query block, chunk) triples x kv heads: the grid
+  int plan_capacity;  // work items the plan area holds
   float scale_log2;
 };
 
@@ -150,45 +155,57 @@ __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+// v_mfma_f32_32x32x16_{bf16,f16}: A [32 x 16] lane l holds row l%32, k
+// 8*(l/32)..+7; B [16 x 32] lane l holds column l%32, the same k; C [32 x 32]
+// lane l holds column l%32, rows 8*(i/4) + 4*(l/32) + i%4 for i = 0..15.
+// (The 16x16x32 form runs at half this rate on gfx950.)
 template <typename T>
-struct MMA16;
+struct MMA32;
 template <>
-struct MMA16<bf16_t> {
-  __device__ __forceinline__ static f32x4 mma(const u32x4& a, const u32x4& b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+struct MMA32<bf16_t> {
+  __device__ __forceinline__ static f32x16 mma(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
                                                    0, 0, 0);
   }
   // v_cvt_pk_bf16_f32: round-to-nearest-even, like f32_to_bf16
   __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, bf16x2_t));
   }
+  __device__ __forceinline__ static uint32_t scale2(uint32_t w, float a) {
+    return pack2(__uint_as_float(w << 16) * a, __uint_as_float(w & 0xffff0000u) * a);
+  }
 };
 template <>
-struct MMA16<f16_t> {
-  __device__ __forceinline__ static f32x4 mma(const u32x4& a, const u32x4& b, f32x4 c) {
-    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+struct MMA32<f16_t> {
+  __device__ __forceinline__ static f32x16 mma(const u32x4& a, const u32x4& b, const f32x16& c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
                                                   0, 0);
   }
   __device__ __forceinline__ static uint32_t pack2(float lo, float hi) {
     return __builtin_bit_cast(uint32_t, __builtin_convertvector(f32x2_t{lo, hi}, f16x2_t));
+  }
+  __device__ __forceinline__ static uint32_t scale2(uint32_t w, float a) {
+    const f16x2_t v = __builtin_bit_cast(f16x2_t, w);
+    return pack2((float)v[0] * a, (float)v[1] * a);
   }
 };
 
 // Geometry of the 16-bit kernel for one head_dim.
 template <int D>
 struct G16 {
-  static constexpr int RB = D <= 128 ? 2 : 1;       // 16-row column blocks per wavefront
-  static constexpr int ROWS = NWAVE * 16 * RB;      // query rows per workgroup
+  static constexpr int ROWS = NWAVE * 32;          // query rows per workgroup (32 per wavefront)
   static constexpr int RBYTES = D * 2;              // bytes per K/V row
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
   static constexpr int SWZ = CPR >= 16 ? 15 : CPR - 1;
   static constexpr int TILE_BYTES = KT * RBYTES;    // K (or V) tile
   static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
-  // Ring depth and the occupancy the register budget is built for: two
-  // workgroups per CU at head_dim 128 (2 x 68 KiB of the 160 KiB LDS,
-  // <= 256 VGPRs), three at 64.
-  static constexpr int NS = D <= 128 ? 4 : 2;
-  static constexpr int WAVES = D <= 64 ? 3 : 2;
+  // The occupancy the register budget is built for: two workgroups per CU at
+  // head_dim <= 128 (LDS: 2 x 68 KiB of the 160 KiB at 128; <= 256 VGPRs),
+  // one at 256 (132 KiB, 512 VGPRs).
+  static constexpr int NS = 4;  // V of tile t-1, tiles t and t+1 resident, tile t+2 in flight
+  static constexpr int WAVES = D <= 128 ? 2 : 1;
   static constexpr int IPW = TILE_BYTES / 1024 / NWAVE;  // 1 KiB transfers per wavefront, each of K and V
   static constexpr int LDS_BYTES = NS * STAGE_BYTES + kWin * 4;
   static_assert(TILE_BYTES % (1024 * NWAVE) == 0, "a tile must split evenly over the wavefronts");
@@ -199,16 +216,29 @@ struct G16 {
 // rows 4g..4g+3 x chunks {2t, 2t+1} land in 8 different ones.
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | (((r >> 2) & 1) << 3) | ((r >> 3) & 1); }
 
+// Instruction order hint for a basic block: DS LDS reads first, then NM MFMAs
+// each followed by VPM VALU instructions of the same wavefront, so the matrix
+// pipe and the VALU run concurrently (a run of MFMAs would block the
+// wavefront's issue until the pipe drains).
+template <int DS, int NM, int VPM>
+__device__ __forceinline__ void sched_interleave() {
+  __builtin_amdgcn_sched_group_barrier(0x100, DS, 0);
+#pragma unroll
+  for (int k = 0; k < NM; ++k) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
+  }
+}
+
 template <typename T, int D, int G>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAVES))) void prefill16_kernel(
     PrefillParams p) {
   using Geo = G16<D>;
-  constexpr int RB = Geo::RB;
   constexpr int ROWS = Geo::ROWS;
   static_assert(ROWS % G == 0, "group must divide the row block");
   constexpr int BQ = ROWS / G;  // query tokens per workgroup
-  constexpr int NQF = D / 32;   // 32-wide d slices of the S^T product
-  constexpr int NDT = D / 16;   // 16-wide output column tiles
+  constexpr int NQF = D / 16;   // 16-wide d steps of the S^T product
+  constexpr int NDT = D / 32;   // 32-wide output column tiles
   constexpr int NS = Geo::NS;
   constexpr int IPW = Geo::IPW;
   constexpr int RBYTES = Geo::RBYTES;
@@ -219,16 +249,10 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAV
   int* slots = reinterpret_cast<int*>(smem + NS * Geo::STAGE_BYTES);
   const uint32_t lds0 = (uint32_t)(uintptr_t)((MSGL_LDS uint8_t*)smem);
 
-  // ---- logical work item (XCD-contiguous ranges) ----
-  const int per_xcd = gridDim.x >> 3;
-  const int lid = (blockIdx.x & 7) * per_xcd + (blockIdx.x >> 3);
-  if (lid >= p.items) return;
-  const int qblk = lid % p.nqb;
-  int rest = lid / p.nqb;
-  const int split = rest % p.splits;
-  rest /= p.splits;
-  const int req = rest % p.num_reqs;
-  const int kvh = rest / p.num_reqs;
+  // ---- work item from the plan (workgroups past its end have nothing to do) ----
+  if ((int)blockIdx.x >= *p.plan_count) return;
+  const int4 item = p.plan[blockIdx.x];
+  const int req = item.x, kvh = item.y, qblk = item.z, split = item.w;
 
   const int q0 = p.q_indptr[req];
   const int E = p.q_indptr[req + 1] - q0;
@@ -247,241 +271,348 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAV
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int col = lane & 15;  // S^T column = query row within a 16-row block
-  const int grp = lane >> 4;  // key group
+  const int rl = lane & 31;  // this lane's query row within the wavefront's 32 (S^T column)
+  const int h = lane >> 5;   // k half of the MFMA operands; row quarter of the results
 
-  // this lane's query rows (one per column block), clamped into range so every
-  // row sees key 0; rows past E are computed, not stored
-  int limit[RB];
-  u32x4 qf[RB][NQF];
-#pragma unroll
-  for (int b = 0; b < RB; ++b) {
-    const int row = (wave * RB + b) * 16 + col;
-    const int tok = min(qb + row / G, E - 1);
-    limit[b] = P + tok;
+  // this lane's query row, clamped into range so every row sees key 0; rows
+  // past E are computed, not stored
+  const int my_row = wave * 32 + rl;
+  const int my_tok = min(qb + my_row / G, E - 1);
+  const int limit = P + my_tok;
+  const int lim_lo = __builtin_amdgcn_readfirstlane(limit);  // the wavefront's first row (lane 0)
+  // Q fragment (B operand of S^T = K Q^T): d = 16j + 8h .. +7
+  u32x4 qf[NQF];
+  {
     const uint8_t* qrow =
-        reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * RBYTES;
+        reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + my_tok) * p.hq + kvh * G + my_row % G) * RBYTES;
 #pragma unroll
-    for (int j = 0; j < NQF; ++j) qf[b][j] = ld16(qrow + (32 * j + 8 * grp) * 2);
+    for (int j = 0; j < NQF; ++j) qf[j] = ld16(qrow + (16 * j + 8 * h) * 2);
   }
-  // smallest visible-key limit of each column block (its first row, lane 0)
-  int lim_lo[RB];
-#pragma unroll
-  for (int b = 0; b < RB; ++b) lim_lo[b] = __builtin_amdgcn_readfirstlane(limit[b]);
   // Q must have arrived before the key loop: otherwise the compiler's wait for
   // it lands inside the loop (its wait analysis merges the loop entry), where a
   // vmcnt would also drain the LDS transfers in flight.
 #pragma unroll
-  for (int b = 0; b < RB; ++b)
-#pragma unroll
-    for (int j = 0; j < NQF; ++j) asm volatile("" ::"v"(qf[b][j]));
+  for (int j = 0; j < NQF; ++j) asm volatile("" ::"v"(qf[j]));
 
-  f32x4 acc[RB][NDT];
-  float m_run[RB], l_run[RB];
+  // O accumulators: acc[dt][i] = O[row 8(i/4) + 4h + i%4][column 32 dt + rl]
+  f32x16 acc[NDT];
 #pragma unroll
-  for (int b = 0; b < RB; ++b) {
-    m_run[b] = -INFINITY;
-    l_run[b] = 0.f;
+  for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-    for (int t = 0; t < NDT; ++t) acc[b][t] = f32x4{0.f, 0.f, 0.f, 0.f};
-  }
+    for (int i = 0; i < 16; ++i) acc[dt][i] = 0.f;
+  float m_run = -INFINITY, l_run = 0.f;  // of this lane's row (l_run: this lane's keys only)
 
   const uint8_t* kp = reinterpret_cast<const uint8_t*>(p.k_pool);
   const uint8_t* vp = reinterpret_cast<const uint8_t*>(p.v_pool);
   const int64_t row_stride = (int64_t)p.hkv * RBYTES;
   const int64_t head_off = (int64_t)kvh * RBYTES;
 
-  // Tile t of the window into ring stage st: this wavefront's IPW transfers of
-  // K and of V. Transfer qi covers LDS bytes [qi KiB, (qi+1) KiB) of the tile:
-  // lane l fills physical chunk (qi*64 + l) % CPR of row (qi*64 + l) / CPR with
-  // logical chunk pc ^ swz(row). Rows past the window repeat its last key.
-  auto issue = [&](int t, int st, int nw) {
+  // This wavefront's IPW transfers of each of K and V per tile. Transfer qi
+  // covers LDS bytes [qi KiB, (qi+1) KiB) of the tile: lane l fills physical
+  // chunk (qi*64 + l) % CPR of row (qi*64 + l) / CPR with logical chunk
+  // pc ^ swz(row). The rows' slots are read from LDS one tile ahead (load_slots)
+  // so the issue itself waits on nothing; rows past the window repeat its last key.
+  int dma_row[IPW], nslot[IPW];
+  const uint8_t* kcol[IPW];
+#pragma unroll
+  for (int i = 0; i < IPW; ++i) {
+    const int flat = (wave + NWAVE * i) * 64 + lane;
+    dma_row[i] = flat / CPR;
+    kcol[i] = kp + head_off + (((flat % CPR) ^ (swz(dma_row[i]) & SWZ)) << 4);
+  }
+  const int64_t vk = vp - kp;  // V rows sit at the same offsets in the V pool
+  auto load_slots = [&](int t, int nw) {
+#pragma unroll
+    for (int i = 0; i < IPW; ++i) nslot[i] = slots[min(t * KT + dma_row[i], nw - 1)];
+  };
+  auto issue = [&](int st) {
     const uint32_t sb = lds0 + st * Geo::STAGE_BYTES;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
-      const int qi = wave + NWAVE * i;
-      const int flat = qi * 64 + lane;
-      const int r = flat / CPR;
-      const int c = (flat % CPR) ^ (swz(r) & SWZ);
-      const int key = min(t * KT + r, nw - 1);
-      const int64_t off = (int64_t)slots[key] * row_stride + head_off + c * 16;
-      const uint32_t lk = __builtin_amdgcn_readfirstlane(sb + qi * 1024);
-      dma16(kp + off, lk);
-      dma16(vp + off, lk + Geo::TILE_BYTES);
+      const uint8_t* g = kcol[i] + (int64_t)nslot[i] * row_stride;
+      const uint32_t lk = __builtin_amdgcn_readfirstlane(sb + (wave + NWAVE * i) * 1024);
+      dma16(g, lk);
+      dma16(g + vk, lk + Geo::TILE_BYTES);
     }
   };
-  // Wait until this wavefront's transfers of a tile have landed, `after` tiles
-  // having been issued behind it.
+  // Wait until this wavefront's transfers of a tile have landed, `after`
+  // (0 or 1) tiles having been issued behind it.
   auto wait_tile = [&](int after) {
     if (after <= 0) {
       vm_wait<0>();
-    } else if (after == 1) {
-      vm_wait<2 * IPW>();
     } else {
-      vm_wait<4 * IPW>();
+      vm_wait<2 * IPW>();
     }
   };
 
+  // S^T = K Q^T of the tile in ring stage st: lane l gets the scores of row rl
+  // against keys 8c + 4h + r (c, r = 0..3) in sdst[4c + r]
+  // (two independent MFMA chains over even and odd d steps, summed)
+  auto scores = [&](int st, f32x16& sdst) {
+    const uint8_t* krow = smem + st * Geo::STAGE_BYTES + rl * RBYTES;  // A operand: key row rl
+    const int sw = swz(rl) & SWZ;
+    f32x16 s2[2];
+#pragma unroll
+    for (int c = 0; c < 2; ++c)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) s2[c][i] = 0.f;
+#pragma unroll
+    for (int j = 0; j < NQF; ++j) {
+      const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (((2 * j + h) ^ sw) << 4));
+      s2[j & 1] = MMA32<T>::mma(a, qf[j], s2[j & 1]);
+    }
+    sdst = s2[0] + s2[1];
+  };
+  // Row max of the scores of tile t (keys kbase..), raw (scale > 0, so the raw
+  // max orders like the scaled one); x gets the scores, -inf where masked.
+  auto rowmax_full = [&](const f32x16& sc, float (&x)[16]) {
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = sc[i];
+      m = fmaxf(m, x[i]);
+    }
+    return m;
+  };
+  auto rowmax_masked = [&](const f32x16& sc, float (&x)[16], int kbase, int kend) {
+    // key 8(i/4) + 4h + i%4 of the tile is visible iff it is <= thr
+    const int thr = min(limit, kend - 1) - kbase - 4 * h;
+    float m = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = 8 * (i >> 2) + (i & 3) <= thr ? sc[i] : -INFINITY;
+      m = fmaxf(m, x[i]);
+    }
+    return m;
+  };
+  // P = exp2(x * scale - m_run) into the A operands of the two 16-key steps of
+  // O += P V: slot (h, e) of step ks = key 16ks + 8(e/4) + 4h + e%4, i.e. this
+  // lane's scores 8ks .. 8ks+7 in order
+  auto probs = [&](const float (&x)[16], u32x4 (&pa)[2]) {
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;  // a row may see nothing yet
+    float pr[16];
+    float lsum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], p.scale_log2, -m_use));
+      lsum += pr[i];
+    }
+    l_run += lsum;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int w = 0; w < 4; ++w) pa[ks][w] = MMA32<T>::pack2(pr[8 * ks + 2 * w], pr[8 * ks + 2 * w + 1]);
+  };
+  // Lazy rescale: a row's reference m_run (log2 domain) moves only when its max
+  // exceeds it by more than 8, so P <= 2^8 and most tiles leave the
+  // accumulators alone. Exact up to rounding: P, l and O share the reference.
+  // The P of the previous tile, whose P V is still to come, is rescaled with
+  // them (in this lane: it holds its own row's P).
+  auto rescale = [&](float mloc, u32x4 (&pa_prev)[2], bool has_prev) {
+    const float mcand = mloc * p.scale_log2;
+    const bool grow = mcand > m_run + 8.f;
+    if (__ballot(grow) != 0) {
+      const float m_new = grow ? mcand : m_run;
+      const float alpha = grow ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+      l_run *= alpha;
+      m_run = m_new;
+      // accumulator i holds row 8(i/4) + 4h + i%4, whose factor is in that lane
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float ar = __shfl(alpha, 8 * (i >> 2) + 4 * h + (i & 3));
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt][i] *= ar;
+      }
+      if (has_prev) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int w = 0; w < 4; ++w) pa_prev[ks][w] = MMA32<T>::scale2(pa_prev[ks][w], alpha);
+      }
+    }
+  };
+  // O += P V with the V tile in ring stage st
+  auto pv = [&](int st, const u32x4 (&pa)[2]) {
+    const uint8_t* Vb = smem + st * Geo::STAGE_BYTES + Geo::TILE_BYTES;
+    // B operand (keys of the same slots x 32 columns) by transposing reads: in
+    // 16-lane group g (columns 16(g%2).., key half h = g/2) source lane i16 reads
+    // row 16ks + 4h + i16/4 (+8 for slots e >= 4), columns 32dt + 16(g%2) + 4(i16%4)
+    // .. +3 = logical chunk 4dt + 2(g%2) + (i16%4)/2, half i16%2
+    const int i16 = lane & 15;
+    const int gs = (lane >> 4) & 1;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int r0 = 16 * ks + 4 * h + (i16 >> 2);
+      const int r1 = r0 + 8;
+      const uint8_t* v0 = Vb + r0 * RBYTES + ((i16 & 1) << 3);
+      const uint8_t* v1 = Vb + r1 * RBYTES + ((i16 & 1) << 3);
+      const int sw0 = swz(r0) & SWZ, sw1 = swz(r1) & SWZ;
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const int c = 4 * dt + 2 * gs + ((i16 & 3) >> 1);
+        const uint2 lo = lds_read_tr16<T>(v0 + ((c ^ sw0) << 4));
+        const uint2 hi = lds_read_tr16<T>(v1 + ((c ^ sw1) << 4));
+        const u32x4 bop = {lo.x, lo.y, hi.x, hi.y};
+        acc[dt] = MMA32<T>::mma(pa[ks], bop, acc[dt]);
+      }
+    }
+  };
+  // Software pipeline per window, three tiles deep. Iteration t:
+  //   A: the S MFMAs of tile t+1 interleaved with tile t's masked row max;
+  //   B: (rare) the rescale when a row's max moved;
+  //   C: the P V MFMAs of tile t-1 interleaved with tile t's exp/sum/pack.
+  // (gfx950 overlaps MFMA with VALU work of the same wavefront, not of other
+  // wavefronts on the SIMD.) V of tile t-1, tile t and K of tile t+1 stay
+  // resident, so iteration t's transfer (tile t+2) fills the stage of tile
+  // t-2: a ring of NS >= 4.
+  static_assert(NS >= 4, "the pipeline keeps three tiles resident");
   for (int w0 = c0; w0 < c1; w0 += kWin) {
     const int nw = min(kWin, c1 - w0);
     const int ntiles = (nw + KT - 1) / KT;
+    const int kend = w0 + nw;
     __syncthreads();  // every wavefront is done with the previous window
     for (int i = tid; i < nw; i += 256) slots[i] = (int)kv_slot(p, kv_start, w0 + i);
     __syncthreads();
 #pragma unroll
-    for (int s = 0; s < NS - 1; ++s)
-      if (s < ntiles) issue(s, s, nw);
+    for (int s = 0; s < 2; ++s)
+      if (s < ntiles) {
+        load_slots(s, nw);
+        issue(s);
+      }
+    load_slots(2, nw);  // clamped into the window: harmless when unused
+    wait_tile(min(1, ntiles - 1));
+    __syncthreads();  // tile 0 visible to all
+    f32x16 s_cur;
+    scores(0, s_cur);
+    u32x4 pa_prev[2];
 
-    for (int t = 0; t < ntiles; ++t) {
-      wait_tile(min(NS - 2, ntiles - 1 - t));
-      __syncthreads();  // tile t visible to all; everyone is done with tile t-1's stage
-      if (t + NS - 1 < ntiles) issue(t + NS - 1, (t + NS - 1) % NS, nw);
-
-      const uint8_t* Kb = smem + (t % NS) * Geo::STAGE_BYTES;
-      const uint8_t* Vb = Kb + Geo::TILE_BYTES;
+    auto iteration = [&](int t, auto first) {
+      constexpr bool FIRST = decltype(first)::value;
+      if (t + 1 < ntiles) vm_wait<0>();  // tile t+1, the only one in flight, landed
+      __syncthreads();  // tile t+1 visible; everyone is done with tile t-2's stage
+      if (t + 2 < ntiles) issue((t + 2) % NS);
       const int kbase = w0 + t * KT;
-      const int kend = w0 + nw;
-
-      // ---- S^T = K Q^T for two 16-key halves, each K fragment feeding RB blocks ----
-      f32x4 s[2][RB];
-#pragma unroll
-      for (int kt = 0; kt < 2; ++kt) {
-        const int r = kt * 16 + col;
-        const uint8_t* krow = Kb + r * RBYTES;
-        const int sw = swz(r) & SWZ;
-#pragma unroll
-        for (int b = 0; b < RB; ++b) s[kt][b] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int j = 0; j < NQF; ++j) {
-          const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (((4 * j + grp) ^ sw) << 4));
-#pragma unroll
-          for (int b = 0; b < RB; ++b) s[kt][b] = MMA16<T>::mma(a, qf[b][j], s[kt][b]);
-        }
+      // A (past the last tile, scores reads a stage whose transfers have all landed; unused)
+      f32x16 s_next;
+      float x[16];
+      float mloc;
+      if (kbase + KT <= kend && kbase + KT - 1 <= lim_lo) {
+        scores((t + 1) % NS, s_next);
+        mloc = rowmax_full(s_cur, x);
+        sched_interleave<NQF, NQF, 2>();
+      } else {
+        scores((t + 1) % NS, s_next);
+        mloc = rowmax_masked(s_cur, x, kbase, kend);
+        sched_interleave<NQF, NQF, 4>();
       }
+      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));  // the row's other 16 keys
+      // B
+      rescale(mloc, pa_prev, !FIRST);
+      // C
+      u32x4 pa_new[2];
+      if constexpr (!FIRST) pv((t - 1) % NS, pa_prev);
+      probs(x, pa_new);
+      load_slots(t + 3, nw);  // for the next iteration's issue (clamped: harmless when unused)
+      if constexpr (!FIRST) sched_interleave<4 * NDT + IPW, 2 * NDT, 6>();
+      pa_prev[0] = pa_new[0];
+      pa_prev[1] = pa_new[1];
+      s_cur = s_next;
+    };
+    iteration(0, std::true_type{});
+    for (int t = 1; t < ntiles; ++t) iteration(t, std::false_type{});
+    pv((ntiles - 1) % NS, pa_prev);
+  }
 
-      // ---- online softmax per column block; P packed as the A operand ----
-      const bool tail = kbase + KT > kend;  // the tile runs past the key range
-      u32x4 pa[RB];
+  // ---- results: accumulator i is WG row wave*32 + 8(i/4) + 4h + i%4, column 32dt + rl ----
+  const float l_row = l_run + __shfl_xor(l_run, 32);  // both halves of this lane's row
+  if (nchunks == 1) {
+    const float inv = 1.f / l_row;
+    T* out = reinterpret_cast<T*>(p.out);
 #pragma unroll
-      for (int b = 0; b < RB; ++b) {
-        // raw scores; masking only where some row of the block misses a key
-        float x[2][4];
-        float mloc = -INFINITY;
-        if (!tail && kbase + KT - 1 <= lim_lo[b]) {
+    for (int i = 0; i < 16; ++i) {
+      const int m = 8 * (i >> 2) + 4 * h + (i & 3);
+      const int row = wave * 32 + m;
+      const int tok = qb + row / G;
+      const float rinv = __shfl(inv, m);
+      if (tok < E) {
+        T* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              x[kt][i] = s[kt][b][i];
-              mloc = fmaxf(mloc, x[kt][i]);
-            }
-        } else {
-#pragma unroll
-          for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const int key = kbase + kt * 16 + 4 * grp + i;
-              const bool vis = key <= limit[b] && key < kend;
-              x[kt][i] = vis ? s[kt][b][i] : -INFINITY;
-              mloc = fmaxf(mloc, x[kt][i]);
-            }
-        }
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 16));
-        mloc = fmaxf(mloc, __shfl_xor(mloc, 32));
-        // Lazy rescale (scale > 0, so the raw max orders like the scaled one):
-        // a row's reference m_run (log2 domain) moves only when its max exceeds
-        // it by more than 8, so P <= 2^8 and most tiles leave the accumulators
-        // alone. Exact up to rounding: P, l and O share the reference.
-        const float mcand = mloc * p.scale_log2;
-        const bool grow = mcand > m_run[b] + 8.f;
-        if (__ballot(grow) != 0) {
-          const float m_new = grow ? mcand : m_run[b];
-          const float alpha = grow ? __builtin_amdgcn_exp2f(m_run[b] - m_new) : 1.f;
-          l_run[b] *= alpha;
-          m_run[b] = m_new;
-          // accumulator row 4*grp+i takes the factor of S^T column 4*grp+i
-          float arow[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) arow[i] = __shfl(alpha, 4 * grp + i);
-#pragma unroll
-          for (int t2 = 0; t2 < NDT; ++t2)
-#pragma unroll
-            for (int i = 0; i < 4; ++i) acc[b][t2][i] *= arow[i];
-        }
-        const float m_use = m_run[b] == -INFINITY ? 0.f : m_run[b];  // a row may see nothing yet
-        float pr[2][4];
-        float lsum = 0.f;
-#pragma unroll
-        for (int kt = 0; kt < 2; ++kt)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            pr[kt][i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[kt][i], p.scale_log2, -m_use));
-            lsum += pr[kt][i];
-          }
-        l_run[b] += lsum;
-        // A operand slot (grp, e<4) = key 4*grp+e, (grp, e>=4) = key 16+4*grp+e-4
-        pa[b][0] = MMA16<T>::pack2(pr[0][0], pr[0][1]);
-        pa[b][1] = MMA16<T>::pack2(pr[0][2], pr[0][3]);
-        pa[b][2] = MMA16<T>::pack2(pr[1][0], pr[1][1]);
-        pa[b][3] = MMA16<T>::pack2(pr[1][2], pr[1][3]);
+        for (int dt = 0; dt < NDT; ++dt) orow[32 * dt + rl] = from_f32<T>(acc[dt][i] * rinv);
       }
-
-      // ---- O += P V: source lane col reads row 4*grp + col/4 (+16), columns
-      //      16t + 4*(col%4) .. +3, i.e. logical chunk 2t + (col%4)/2, half col%2 ----
-      const int rlo = 4 * grp + (col >> 2);
-      const int vsw = swz(rlo) & SWZ;  // rlo + 16 has the same swizzle
-      const uint8_t* vrow = Vb + rlo * RBYTES + ((col & 1) << 3);
+    }
+  } else {
+    const int64_t base = (int64_t)split * p.num_tokens;
+    if (h == 0) {
+      const int tok = qb + my_row / G;
+      if (tok < E && q0 + tok < p.num_tokens)
+        p.part_ml[(base + q0 + tok) * p.hq + kvh * G + my_row % G] = make_float2(m_run, l_row);
+    }
 #pragma unroll
-      for (int t2 = 0; t2 < NDT; ++t2) {
-        const int off = ((2 * t2 + ((col >> 1) & 1)) ^ vsw) << 4;
-        const uint2 lo = lds_read_tr16<T>(vrow + off);
-        const uint2 hi = lds_read_tr16<T>(vrow + 16 * RBYTES + off);
-        const u32x4 bop = {lo.x, lo.y, hi.x, hi.y};
+    for (int i = 0; i < 16; ++i) {
+      const int row = wave * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+      const int tok = qb + row / G;
+      if (tok < E && q0 + tok < p.num_tokens) {  // the workspace holds num_tokens rows
+        float* orow = p.part_o + ((base + q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
-        for (int b = 0; b < RB; ++b) acc[b][t2] = MMA16<T>::mma(pa[b], bop, acc[b][t2]);
+        for (int dt = 0; dt < NDT; ++dt) orow[32 * dt + rl] = acc[dt][i];
       }
     }
   }
+}
 
-  // ---- results: accumulator row 4*grp+i of block b is WG row (wave*RB+b)*16 + 4*grp + i ----
-#pragma unroll
-  for (int b = 0; b < RB; ++b) {
-    float l = l_run[b];
-    l += __shfl_xor(l, 16);
-    l += __shfl_xor(l, 32);
-    const int rbase = (wave * RB + b) * 16;
-    if (nchunks == 1) {
-      const float inv = 1.f / l;
-      T* out = reinterpret_cast<T*>(p.out);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = rbase + 4 * grp + i;
-        const int tok = qb + row / G;
-        const float rinv = __shfl(inv, 4 * grp + i);
-        if (tok < E) {
-          T* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
-#pragma unroll
-          for (int t2 = 0; t2 < NDT; ++t2) orow[t2 * 16 + col] = from_f32<T>(acc[b][t2][i] * rinv);
-        }
-      }
-    } else {
-      const int64_t base = (int64_t)split * p.num_tokens;
-      if (grp == 0) {
-        const int row = rbase + col;
-        const int tok = qb + row / G;
-        if (tok < E && q0 + tok < p.num_tokens)
-          p.part_ml[(base + q0 + tok) * p.hq + kvh * G + row % G] = make_float2(m_run[b], l);
-      }
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int row = rbase + 4 * grp + i;
-        const int tok = qb + row / G;
-        if (tok < E && q0 + tok < p.num_tokens) {  // the workspace holds num_tokens rows
-          float* orow = p.part_o + ((base + q0 + tok) * p.hq + kvh * G + row % G) * D;
-#pragma unroll
-          for (int t2 = 0; t2 < NDT; ++t2) orow[t2 * 16 + col] = acc[b][t2][i];
-        }
-      }
+// Work list for prefill16_kernel, one workgroup: every (request, query block,
+// chunk) triple with keys to process, counting-sorted by its tile count
+// (longest first, buckets of 1..255+ tiles) so the hardware dispatcher hands
+// out the long items first, each expanded to the kv heads as consecutive
+// items (consecutive workgroups go to consecutive XCDs, so with 8 kv heads a
+// head's query blocks share one L2). A grid without empty workgroups in the
+// middle keeps every CU slot busy; the list order does not change any result.
+constexpr int kPlanThreads = 1024;
+
+__device__ __forceinline__ int plan_tiles(const PrefillParams& p, int bq, int t, int& req, int& qblk, int& split) {
+  split = t % p.splits;
+  qblk = (t / p.splits) % p.nqb;
+  req = t / (p.splits * p.nqb);
+  const int q0 = p.q_indptr[req];
+  const int E = p.q_indptr[req + 1] - q0;
+  const int qb = qblk * bq;
+  if (qb >= E) return 0;
+  const int L = p.seq_lens ? p.seq_lens[req] : (p.kv_indptr[req + 1] - p.kv_indptr[req]);
+  const int kv_end = block_kv_end(L, E, qb, bq);
+  int n, clen;
+  chunk_geometry(kv_end, p.splits, p.chunk_len, n, clen);
+  if (split >= n) return 0;
+  const int c0 = split * clen;
+  const int c1 = split == n - 1 ? kv_end : c0 + clen;
+  return (c1 - c0 + KT - 1) / KT;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillParams p, int bq) {
+  __shared__ int hist[256];
+  const int ntrip = p.num_reqs * p.nqb * p.splits;
+  for (int b = threadIdx.x; b < 256; b += kPlanThreads) hist[b] = 0;
+  __syncthreads();
+  int req, qblk, split;
+  for (int t = threadIdx.x; t < ntrip; t += kPlanThreads) {
+    const int n = plan_tiles(p, bq, t, req, qblk, split);
+    if (n > 0) atomicAdd(&hist[min(n, 255)], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // exclusive offsets, longest bucket first
+    int run = 0;
+    for (int b = 255; b >= 1; --b) {
+      const int c = hist[b];
+      hist[b] = run;
+      run += c;
+    }
+    *p.plan_count = run * p.hkv;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < ntrip; t += kPlanThreads) {
+    const int n = plan_tiles(p, bq, t, req, qblk, split);
+    if (n > 0) {
+      const int pos = atomicAdd(&hist[min(n, 255)], 1);
+      for (int h = 0; h < p.hkv; ++h) p.plan[pos * p.hkv + h] = make_int4(req, h, qblk, split);
     }
   }
 }
@@ -741,10 +872,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
 // ---------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------
-int tokens_per_block16(int head_dim, int group) {
-  const int rows = head_dim <= 128 ? NWAVE * 32 : NWAVE * 16;
-  return rows / group;
-}
+int tokens_per_block16(int group) { return NWAVE * 32 / group; }
 
 template <typename T, int D, int G>
 int launch16(PrefillParams p, int max_e, hipStream_t stream) {
@@ -752,12 +880,14 @@ int launch16(PrefillParams p, int max_e, hipStream_t stream) {
   constexpr int BQ = Geo::ROWS / G;
   p.nqb = (max_e + BQ - 1) / BQ;
   const int64_t items = (int64_t)p.hkv * p.num_reqs * p.splits * p.nqb;
-  if (items > (int64_t)INT32_MAX - 8) {
-    set_error("msgl_prefill_ragged: %lld workgroups exceed the grid limit", (long long)items);
-    return MSGL_ERR_INVALID;
-  }
   p.items = (int)items;
-  const int grid = (int)((items + 7) / 8 * 8);
+  if (items > (int64_t)p.plan_capacity) {
+    set_error("msgl_prefill_ragged: workspace holds %d work items, %lld needed", p.plan_capacity, (long long)items);
+    return MSGL_ERR_WORKSPACE;
+  }
+  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p, BQ);
+  MSGL_CHECK_LAUNCH("msgl_prefill_ragged (plan)");
+  const int grid = (int)items;
   static bool attr_set = false;  // per process; the attribute is per function
   if (Geo::LDS_BYTES > 65536 && !attr_set) {
     if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill16_kernel<T, D, G>),
@@ -825,6 +955,24 @@ int prefill_dim(const PrefillParams& p, int max_e, int head_dim, int group, hipS
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
+// Workspace of the 16-bit path: plan length, plan (one int4 per work item),
+// then with splits > 1 the per-chunk (m, l) and O partials.
+struct PrefillWorkspace {
+  int64_t items, plan, part_ml, part_o, bytes;
+};
+PrefillWorkspace prefill_workspace(int num_reqs, int num_tokens, int max_e, int hq, int hkv, int head_dim,
+                                   int splits) {
+  PrefillWorkspace w;
+  const int bq = tokens_per_block16(hq / hkv) > 0 ? tokens_per_block16(hq / hkv) : 1;
+  w.items = (int64_t)num_reqs * ((max_e + bq - 1) / bq) * splits * hkv;
+  const int64_t rows = splits > 1 ? (int64_t)splits * num_tokens * hq : 0;
+  w.plan = 256;
+  w.part_ml = w.plan + align256(w.items * 16);
+  w.part_o = w.part_ml + align256(rows * 8);
+  w.bytes = w.part_o + align256(rows * head_dim * 4);
+  return w;
+}
+
 }  // namespace
 }  // namespace msgl
 
@@ -833,22 +981,27 @@ extern "C" int32_t msgl_prefill_default_splits(int32_t num_reqs, int32_t num_qo_
   using namespace msgl;
   if (num_reqs <= 0 || num_kv_heads <= 0 || num_qo_heads < num_kv_heads || max_extend_len <= 0) return 1;
   const int group = num_qo_heads / num_kv_heads;
-  const int bq = tokens_per_block16(head_dim, group) > 0 ? tokens_per_block16(head_dim, group) : 1;
+  const int bq = tokens_per_block16(group) > 0 ? tokens_per_block16(group) : 1;
   const int64_t base = (int64_t)num_reqs * num_kv_heads * ((max_extend_len + bq - 1) / bq);
-  // about 8 resident workgroups' worth per CU of the 256-CU device
-  const int64_t target = 2048;
+  // about 6 workgroups per CU of the 256-CU device (two resident at a time):
+  // enough items to balance, few enough partials to merge
+  const int64_t target = 1536;
   int64_t s = (target + base - 1) / base;
   if (max_seq_len > 0) s = std::min<int64_t>(s, std::max<int64_t>(1, (max_seq_len + kMinChunk - 1) / kMinChunk));
   s = std::max<int64_t>(1, std::min<int64_t>(s, kMaxSplits));
   return (int32_t)s;
 }
 
-extern "C" int64_t msgl_prefill_workspace_size(int32_t num_tokens, int32_t num_qo_heads, int32_t head_dim,
+extern "C" int64_t msgl_prefill_workspace_size(int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
+                                               int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                                                int32_t max_splits) {
   using namespace msgl;
-  if (max_splits <= 1 || num_tokens <= 0 || num_qo_heads <= 0 || head_dim <= 0) return 0;
-  const int64_t rows = (int64_t)max_splits * num_tokens * num_qo_heads;
-  return align256(rows * 8) + align256(rows * head_dim * 4);
+  if (num_reqs <= 0 || num_tokens <= 0 || max_extend_len <= 0 || num_qo_heads <= 0 || num_kv_heads <= 0 ||
+      head_dim <= 0 || num_qo_heads % num_kv_heads != 0 || max_splits < 1)
+    return 0;
+  return prefill_workspace(num_reqs, num_tokens, max_extend_len, num_qo_heads, num_kv_heads, head_dim,
+                           std::min<int32_t>(max_splits, kMaxSplits))
+      .bytes;
 }
 
 extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, const int32_t* q_indptr,
@@ -891,6 +1044,9 @@ extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void
   p.out = out;
   p.part_o = nullptr;
   p.part_ml = nullptr;
+  p.plan = nullptr;
+  p.plan_count = nullptr;
+  p.plan_capacity = 0;
   p.num_slots = num_slots;
   p.hq = num_qo_heads;
   p.hkv = num_kv_heads;
@@ -906,17 +1062,24 @@ extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void
   p.nqb = 0;
   p.items = 0;
   p.scale_log2 = scale * kLog2eP;
-  if (p.splits > 1) {
-    const int64_t need = msgl_prefill_workspace_size(num_tokens, num_qo_heads, head_dim, p.splits);
-    if (workspace == nullptr || workspace_bytes < need) {
-      set_error("msgl_prefill_ragged: workspace of %lld bytes needed for %d splits, got %lld", (long long)need,
+  if (dtype != MSGL_F32) {
+    const PrefillWorkspace w =
+        prefill_workspace(num_reqs, num_tokens, max_extend_len, num_qo_heads, num_kv_heads, head_dim, p.splits);
+    if (workspace == nullptr || workspace_bytes < w.bytes) {
+      set_error("msgl_prefill_ragged: workspace of %lld bytes needed (%d splits), got %lld", (long long)w.bytes,
                 p.splits, (long long)workspace_bytes);
       return MSGL_ERR_WORKSPACE;
     }
     MSGL_CHECK_ARG((uintptr_t)workspace % 256 == 0, "msgl_prefill_ragged: workspace must be 256-byte aligned");
-    const int64_t rows = (int64_t)p.splits * num_tokens * num_qo_heads;
-    p.part_ml = reinterpret_cast<float2*>(workspace);
-    p.part_o = reinterpret_cast<float*>(reinterpret_cast<uint8_t*>(workspace) + align256(rows * 8));
+    MSGL_CHECK_ARG(w.items <= INT32_MAX, "msgl_prefill_ragged: too many work items");
+    uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+    p.plan_count = reinterpret_cast<int*>(ws);
+    p.plan = reinterpret_cast<int4*>(ws + w.plan);
+    p.plan_capacity = (int)w.items;
+    if (p.splits > 1) {
+      p.part_ml = reinterpret_cast<float2*>(ws + w.part_ml);
+      p.part_o = reinterpret_cast<float*>(ws + w.part_o);
+    }
   }
   const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;

@@ -86,7 +86,7 @@ SIGNATURES = {
     ),
     "msgl_table_scatter": (ctypes.c_int, [_c_p, _c_i64, _c_i64, _c_p, _c_p, _c_p, _c_i64, _c_p]),
     "msgl_prefill_default_splits": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
-    "msgl_prefill_workspace_size": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32]),
+    "msgl_prefill_workspace_size": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
 }
 
 _lib = None

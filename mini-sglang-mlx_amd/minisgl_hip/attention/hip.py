@@ -174,6 +174,11 @@ class HipAttnBackend(BaseAttnBackend):
             max_seq_len=d.max_seq_len,
             max_splits=d.max_splits,
             workspace=self._shared_workspace(
-                ops.prefill_workspace_bytes(d.num_tokens, self.config.num_qo_heads, self.config.head_dim, d.max_splits)
+                ops.prefill_workspace_bytes(
+                    d.q_indptr.shape[0] - 1, d.num_tokens, d.max_extend_len, self.config.num_qo_heads,
+                    self.config.num_kv_heads, self.config.head_dim, d.max_splits,
+                )
+                if self.kv_cache.dtype != torch.float32
+                else 0
             ),
         )

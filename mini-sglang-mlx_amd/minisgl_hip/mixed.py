@@ -1,0 +1,108 @@
+"""One continuous-batching step with decode and prefill requests in one packed batch.
+
+The reference never mixes phases in a batch (core.py:102, attention/base.py:49-60
+dispatch on batch.phase); this runner executes both on one stream so a
+scheduler that does mix them pays one metadata build per step:
+
+1. ``msgl_build_step_indices`` from the device page table (positions,
+   out_loc, q offsets and the page-level CSR for every request), the GPU form
+   of scheduler/scheduler.py:154-157 and attention/metal.py:145-152;
+2. the prefill requests' KV store (kvcache/pool.py:47-50);
+3. paged decode over the decode requests with their KV store fused in;
+4. ragged prefill over the prefill chunks (attention/base.py:85-105).
+
+Decode requests come first in the packed batch (one token each), prefill
+requests after them; q and out are the packed [T, Hq, D] tensors. Per request
+the results are those of the reference's decode or prefill path.
+"""
+
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import ops
+
+
+class MixedStep:
+    """Device copies of a step's per-request arrays plus reusable workspaces."""
+
+    def __init__(
+        self,
+        req_to_token: torch.Tensor,
+        table_idx: torch.Tensor,
+        cached_len: torch.Tensor,
+        device_len: torch.Tensor,
+        *,
+        num_decode: int,
+        num_tokens: int,
+        num_pages: int,
+        max_chunk: int,
+        max_seq_len: int,
+        num_qo_heads: int,
+        num_kv_heads: int,
+        head_dim: int,
+        page_size: int,
+        decode_splits: Optional[int] = None,
+        prefill_splits: Optional[int] = None,
+    ) -> None:
+        self.req_to_token = req_to_token
+        self.table_idx = table_idx
+        self.cached_len = cached_len
+        self.device_len = device_len
+        self.num_decode = num_decode
+        self.num_tokens = num_tokens
+        self.num_pages = num_pages
+        self.max_chunk = max_chunk
+        self.max_seq_len = max_seq_len
+        self.page_size = page_size
+        num_reqs = table_idx.shape[0]
+        num_prefill = num_reqs - num_decode
+        dev = req_to_token.device
+        if decode_splits is None:
+            decode_splits = ops.default_splits(max(num_decode, 1), num_kv_heads, max_seq_len)
+        if prefill_splits is None:
+            prefill_splits = (
+                ops.prefill_default_splits(num_prefill, num_qo_heads, num_kv_heads, head_dim, max_chunk, max_seq_len)
+                if num_prefill
+                else 1
+            )
+        self.decode_splits = decode_splits
+        self.prefill_splits = prefill_splits
+        self.decode_ws = ops.decode_workspace(max(num_decode, 1), num_qo_heads, num_kv_heads, head_dim,
+                                              decode_splits, dev)
+        self.prefill_ws = (
+            ops.prefill_workspace(num_prefill, num_tokens, max_chunk, num_qo_heads, num_kv_heads, head_dim,
+                                  prefill_splits, dev)
+            if num_prefill
+            else None
+        )
+        self.indices: Optional[dict] = None
+
+    def build_indices(self) -> dict:
+        self.indices = ops.build_step_indices(
+            self.req_to_token, self.table_idx, self.cached_len, self.device_len,
+            num_tokens=self.num_tokens, num_kv=self.num_pages, page_size=self.page_size,
+        )
+        return self.indices
+
+    def run(self, q, k_new, v_new, k_pool, v_pool, out, scale: float) -> torch.Tensor:
+        """q, k_new, v_new, out: packed [T, H, D]; the pools are one layer's."""
+        idx = self.build_indices()
+        nd = self.num_decode
+        if self.num_tokens > nd:
+            ops.store_kv(k_new[nd:], v_new[nd:], idx["out_loc"][nd:], k_pool, v_pool)
+        if nd:
+            ops.paged_decode_attention(
+                q[:nd], k_pool, v_pool, idx["kv_indptr"][: nd + 1], idx["kv_indices"], scale,
+                seq_lens=self.device_len[:nd], page_size=self.page_size, max_splits=self.decode_splits,
+                out=out[:nd], workspace=self.decode_ws, new_kv=(k_new[:nd], v_new[:nd], idx["out_loc"][:nd]),
+            )
+        if self.num_tokens > nd:
+            ops.prefill_ragged_attention(
+                q, k_pool, v_pool, idx["q_indptr"][nd:], idx["kv_indptr"][nd:], idx["kv_indices"],
+                self.device_len[nd:], scale, max_extend_len=self.max_chunk, max_seq_len=self.max_seq_len,
+                page_size=self.page_size, max_splits=self.prefill_splits, out=out, workspace=self.prefill_ws,
+            )
+        return out

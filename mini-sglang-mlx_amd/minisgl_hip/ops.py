@@ -83,14 +83,20 @@ def prefill_default_splits(num_reqs: int, num_qo_heads: int, num_kv_heads: int, 
                                                        max_extend_len, max_seq_len))
 
 
-def prefill_workspace_bytes(num_tokens: int, num_qo_heads: int, head_dim: int, max_splits: int) -> int:
-    return int(_lib.load().msgl_prefill_workspace_size(num_tokens, num_qo_heads, head_dim, max_splits))
+def prefill_workspace_bytes(num_reqs: int, num_tokens: int, max_extend_len: int, num_qo_heads: int,
+                            num_kv_heads: int, head_dim: int, max_splits: int) -> int:
+    return int(_lib.load().msgl_prefill_workspace_size(num_reqs, num_tokens, max_extend_len, num_qo_heads,
+                                                       num_kv_heads, head_dim, max_splits))
 
 
-def prefill_workspace(num_tokens: int, num_qo_heads: int, head_dim: int, max_splits: int,
-                      device) -> Optional[torch.Tensor]:
-    """A workspace for ``prefill_ragged_attention`` (None when no split)."""
-    need = prefill_workspace_bytes(num_tokens, num_qo_heads, head_dim, max_splits)
+def prefill_workspace(num_reqs: int, num_tokens: int, max_extend_len: int, num_qo_heads: int, num_kv_heads: int,
+                      head_dim: int, max_splits: int, device) -> Optional[torch.Tensor]:
+    """A workspace for ``prefill_ragged_attention`` (bf16/fp16).
+
+    Consecutive calls on one stream may reuse it; overlapping calls may not.
+    """
+    need = prefill_workspace_bytes(num_reqs, num_tokens, max_extend_len, num_qo_heads, num_kv_heads, head_dim,
+                                   max_splits)
     if need == 0:
         return None
     return torch.empty(need, dtype=torch.uint8, device=device)
@@ -238,7 +244,8 @@ def prefill_ragged_attention(
     lib = _lib.load()
     if max_splits is None:
         max_splits = prefill_default_splits(num_reqs, hq, hkv, d, int(max_extend_len), int(max_seq_len))
-    need = prefill_workspace_bytes(t, hq, d, max_splits) if q.dtype != torch.float32 else 0
+    need = (prefill_workspace_bytes(num_reqs, t, int(max_extend_len), hq, hkv, d, max_splits)
+            if q.dtype != torch.float32 else 0)
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()

@@ -219,3 +219,82 @@ def prefill_flops_bytes(prefix_lens, extend_lens, hq: int, hkv: int, d: int, ele
     flops = 4 * hq * d * int(np.sum(e * p + e * (e + 1) // 2))
     nbytes = int(np.sum(p + e)) * hkv * d * elem * 2 + int(e.sum()) * hq * d * elem * 2
     return flops, nbytes
+
+
+@dataclass
+class MixedCase:
+    """A continuous-batching step over one token-granular page table.
+
+    Requests 0..num_decode-1 decode one token (cached_len = L - 1, device_len =
+    L); the others extend a chunk over a cached prefix. ``req_to_token`` is the
+    scheduler's page table (core.py:126-127, engine/engine.py:74) with requests
+    on shuffled rows ``table_idx``; each request's pages are consecutive slices
+    of one random permutation of the pool's pages (scheduler/cache.py:138-143).
+    Positions [cached_len, device_len) of every request are this step's tokens,
+    their slots already allocated in the table (scheduler/cache.py:53-72).
+    """
+
+    req_to_token: np.ndarray  # [num_rows, max_len] int32
+    table_idx: np.ndarray  # [R] int32
+    cached_len: np.ndarray  # [R] int32
+    device_len: np.ndarray  # [R] int32
+    num_decode: int
+    page_size: int
+    num_slots: int
+
+    @property
+    def num_reqs(self) -> int:
+        return int(self.device_len.shape[0])
+
+    @property
+    def num_tokens(self) -> int:
+        return int((self.device_len - self.cached_len).sum())
+
+    @property
+    def num_pages(self) -> int:
+        return int(sum(_div_ceil(int(n), self.page_size) for n in self.device_len))
+
+    @property
+    def max_chunk(self) -> int:
+        e = self.device_len[self.num_decode :] - self.cached_len[self.num_decode :]
+        return int(e.max()) if len(e) else 0
+
+    def slots(self, i: int) -> np.ndarray:
+        """Token slots of request i's full context (table row, first device_len entries)."""
+        return self.req_to_token[self.table_idx[i], : int(self.device_len[i])]
+
+
+def mixed_case(
+    num_decode: int,
+    dec_lo: int,
+    dec_hi: int,
+    prefill_prefixes,
+    chunk: int,
+    num_slots: int,
+    page_size: int = 16,
+    seed: int = 0,
+) -> MixedCase:
+    """num_decode decode requests with L ~ U_int[dec_lo, dec_hi], then one chunk of
+    ``chunk`` tokens over each prefix in ``prefill_prefixes``."""
+    rng = np.random.default_rng(seed)
+    dec = rng.integers(dec_lo, dec_hi + 1, size=num_decode).astype(np.int64)
+    pre = np.asarray(prefill_prefixes, dtype=np.int64)
+    device_len = np.concatenate([dec, pre + chunk]).astype(np.int32)
+    cached_len = np.concatenate([dec - 1, pre]).astype(np.int32)
+    r = len(device_len)
+    num_pages = num_slots // page_size
+    need = sum(_div_ceil(int(n), page_size) for n in device_len)
+    if need > num_pages:
+        raise ValueError(f"pool of {num_slots} slots too small for {need} pages")
+    perm = rng.permutation(num_pages).astype(np.int64)
+    num_rows = r + 2
+    max_len = _div_ceil(int(device_len.max()), page_size) * page_size
+    table = np.zeros((num_rows, max_len), dtype=np.int32)
+    table_idx = rng.permutation(num_rows)[:r].astype(np.int32)
+    off = 0
+    for i, n in enumerate(device_len):
+        p = _div_ceil(int(n), page_size)
+        pages = perm[off : off + p]
+        off += p
+        table[table_idx[i], : p * page_size] = (pages[:, None] * page_size + np.arange(page_size)).reshape(-1)
+    return MixedCase(table, table_idx, cached_len, device_len, num_decode, page_size, num_slots)

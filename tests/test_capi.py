@@ -52,12 +52,16 @@ def test_abi_version_and_sizes():
 def test_prefill_sizes():
     lib = _lib.load()
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert lib.msgl_prefill_workspace_size(2048, 16, 128, 1) == 0
+    # (R, T, maxE, Hq, Hkv, D, splits): 128 query rows per work item, so 64 tokens at Hq/Hkv = 2
+    items = 16 * 8 * 8  # requests x query blocks (ceil(512 / 64)) x kv heads
+    assert lib.msgl_prefill_workspace_size(16, 2048, 512, 16, 8, 128, 1) == 256 + up(items * 16)
     rows = 4 * 2048 * 16
-    assert lib.msgl_prefill_workspace_size(2048, 16, 128, 4) == up(rows * 8) + up(rows * 128 * 4)
-    # 16 requests x 8 kv heads x ceil(512 / 64) blocks = 1024 workgroups: two chunks reach 2048
+    assert lib.msgl_prefill_workspace_size(16, 2048, 512, 16, 8, 128, 4) == (
+        256 + up(4 * items * 16) + up(rows * 8) + up(rows * 128 * 4))
+    assert lib.msgl_prefill_workspace_size(16, 2048, 512, 16, 6, 128, 4) == 0  # Hq not a multiple of Hkv
+    # 16 requests x 8 kv heads x ceil(512 / 64) blocks = 1024 workgroups: two chunks reach 1536
     assert lib.msgl_prefill_default_splits(16, 16, 8, 128, 512, 4096) == 2
-    assert lib.msgl_prefill_default_splits(16, 16, 8, 128, 199, 4160) == 4
+    assert lib.msgl_prefill_default_splits(16, 16, 8, 128, 199, 4160) == 3
     assert lib.msgl_prefill_default_splits(1, 32, 8, 128, 64, 100000) == 16  # capped at 16
     assert lib.msgl_prefill_default_splits(1, 32, 8, 128, 64, 300) == 2  # >= 256 keys per chunk
     assert lib.msgl_prefill_default_splits(0, 32, 8, 128, 64, 300) == 1
@@ -90,8 +94,9 @@ def test_host_side_argument_errors():
     assert pf(0, 0) == _lib.MSGL_ERR_INVALID and "max_splits" in _lib.last_error()
     assert pf(17, 0) == _lib.MSGL_ERR_INVALID
     assert pf(4, 0) == _lib.MSGL_ERR_WORKSPACE
+    assert pf(1, 0) == _lib.MSGL_ERR_WORKSPACE  # bf16 always needs the work-list workspace
     assert pf(4, 1 << 30, d=96) == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
-    assert pf(4, 0, dtype=0, d=96) == _lib.MSGL_ERR_UNSUPPORTED  # fp32 ignores splits: no workspace needed
+    assert pf(4, 0, dtype=0, d=96) == _lib.MSGL_ERR_UNSUPPORTED  # fp32 needs no workspace: reaches dispatch
     assert lib.msgl_prefill_ragged(nul, nul, nul, nul, nul, nul, nul, 0, 0, 0, 0, 16, 8, 128, 1, 100, 1, 0.1, 1,
                                    nul, nul, 0, nul) == _lib.MSGL_OK
     # step indices: (table, rows, stride, table_idx, cached, device_len, R, page, q_indptr, positions, out_loc,

@@ -1,0 +1,109 @@
+"""A continuous-batching step mixing decode and prefill requests (indices built
+on the GPU from the page table) vs the float64 oracle, request by request:
+decode requests as attention/naive.py:50-60, prefill chunks as
+attention/base.py:85-105, the step's KV rows as kvcache/pool.py:47-50."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import assert_close, i32, randn, to_np64
+from minisgl_hip import workloads
+from minisgl_hip.mixed import MixedStep
+
+pytestmark = pytest.mark.gpu
+
+HQ, HKV, D = 32, 8, 128
+SCALE = D**-0.5
+
+
+def _step(case, device, max_seq_len):
+    return MixedStep(
+        i32(case.req_to_token, device), i32(case.table_idx, device), i32(case.cached_len, device),
+        i32(case.device_len, device), num_decode=case.num_decode, num_tokens=case.num_tokens,
+        num_pages=case.num_pages, max_chunk=case.max_chunk, max_seq_len=max_seq_len, num_qo_heads=HQ,
+        num_kv_heads=HKV, head_dim=D, page_size=case.page_size,
+    )
+
+
+def _rows(pool, slots):
+    return to_np64(pool.index_select(0, torch.from_numpy(np.asarray(slots, np.int64)).to(pool.device)))
+
+
+def _check_request(case, i, q, kp, vp, out, rows=None):
+    """Request i of the step vs the oracle (rows: extend rows to check, default all)."""
+    slots = case.slots(i)
+    kb, vb = _rows(kp, slots), _rows(vp, slots)
+    t0 = int((case.device_len[:i] - case.cached_len[:i]).sum())
+    e = int(case.device_len[i] - case.cached_len[i])
+    if i < case.num_decode:
+        ref = oracle.paged_decode(to_np64(q[t0 : t0 + 1]), kb, vb, np.array([0, len(slots)]),
+                                  np.arange(len(slots)), SCALE)
+        assert_close(out[t0 : t0 + 1], ref, torch.bfloat16, f"mixed decode request {i}")
+        return
+    n = e if rows is None else rows
+    # bottom-right causal: query t sees keys <= P + t whatever E is, so the first
+    # n rows of the chunk equal a request truncated to n extend tokens
+    keep = int(case.cached_len[i]) + n
+    ref = oracle.forward_prefill(to_np64(q[t0 : t0 + n]), None, None, kb[:keep], vb[:keep], [0, n],
+                                 [np.arange(keep)], SCALE)
+    assert_close(out[t0 : t0 + n], ref, torch.bfloat16, f"mixed prefill request {i} rows<{n}")
+    # and the chunk's last row sees the whole context (a single query, no mask)
+    ref_last = oracle.forward_prefill(to_np64(q[t0 + e - 1 : t0 + e]), None, None, kb, vb, [0, 1],
+                                      [np.arange(len(slots))], SCALE)
+    assert_close(out[t0 + e - 1 : t0 + e], ref_last, torch.bfloat16, f"mixed prefill request {i} last row")
+
+
+def test_mixed_step_small(cuda_device):
+    """8 decode requests (L in [20, 600]) + chunks of 64 over prefixes 0 and 300, page 16."""
+    case = workloads.mixed_case(8, 20, 600, [0, 300], 64, num_slots=16384, page_size=16, seed=7)
+    print("case mixed small", flush=True)
+    dt = torch.bfloat16
+    kp = randn((case.num_slots, HKV, D), 60, dt).to(cuda_device)
+    vp = randn((case.num_slots, HKV, D), 61, dt).to(cuda_device)
+    t = case.num_tokens
+    q = randn((t, HQ, D), 62, dt).to(cuda_device)
+    kn = randn((t, HKV, D), 63, dt).to(cuda_device)
+    vn = randn((t, HKV, D), 64, dt).to(cuda_device)
+    out = torch.empty_like(q)
+    step = _step(case, cuda_device, int(case.device_len.max()))
+    step.run(q, kn, vn, kp, vp, out, SCALE)
+    torch.cuda.synchronize()
+    # the step's rows are in the pool at the slots of positions [cached, device)
+    positions, out_loc = oracle.prepare_batch_indices(case.req_to_token, case.table_idx, case.cached_len,
+                                                      case.device_len)
+    np.testing.assert_array_equal(step.indices["out_loc"].cpu().numpy(), out_loc)
+    sl = torch.from_numpy(out_loc.astype(np.int64)).to(cuda_device)
+    assert torch.equal(kp.index_select(0, sl), kn) and torch.equal(vp.index_select(0, sl), vn)
+    for i in range(case.num_reqs):
+        _check_request(case, i, q, kp, vp, out)
+
+
+def test_mixed_step_full_size(cuda_device):
+    """128 decode requests with contexts 512..32768, chunks of 1024 over prefixes 0 and
+    8192, Qwen3-8B heads, page 16, a pool of 8M slots (32 GiB): sampled requests."""
+    case = workloads.mixed_case(128, 512, 32768, [0, 8192], 1024, num_slots=8 << 20, page_size=16, seed=0)
+    print("case mixed full", flush=True)
+    dt = torch.bfloat16
+    g = torch.Generator(device=cuda_device).manual_seed(70)
+    kp = torch.randn((case.num_slots, HKV, D), generator=g, device=cuda_device, dtype=dt)
+    vp = torch.randn((case.num_slots, HKV, D), generator=g, device=cuda_device, dtype=dt)
+    t = case.num_tokens
+    q = torch.randn((t, HQ, D), generator=g, device=cuda_device, dtype=dt)
+    kn = torch.randn((t, HKV, D), generator=g, device=cuda_device, dtype=dt)
+    vn = torch.randn((t, HKV, D), generator=g, device=cuda_device, dtype=dt)
+    out = torch.empty_like(q)
+    step = _step(case, cuda_device, int(case.device_len.max()))
+    step.run(q, kn, vn, kp, vp, out, SCALE)
+    out2 = torch.empty_like(q)
+    step.run(q, kn, vn, kp, vp, out2, SCALE)
+    torch.cuda.synchronize()
+    assert torch.equal(out, out2), "mixed step is not deterministic"
+    longest = int(np.argmax(case.device_len[: case.num_decode]))
+    for i in sorted({0, 5, longest, case.num_decode - 1}):
+        _check_request(case, i, q, kp, vp, out)
+    for i in (case.num_decode, case.num_decode + 1):
+        _check_request(case, i, q, kp, vp, out, rows=64)
+    del kp, vp
+    torch.cuda.empty_cache()
