@@ -168,16 +168,19 @@ def bench_decode(args, dev):
     scale = D**-0.5
 
     def step(timed_layer=-1, events=None):
-        # per layer: the KV store of the new token fused into the paged-decode
-        # launch (msgl_paged_decode_store), then the split-K merge. One layer per
-        # step is bracketed by HIP events (an event record costs a queue
-        # barrier, so recording around every layer would slow the step down).
+        # the step's decode work list is planned once (msgl_paged_decode_plan),
+        # then per layer: the KV store of the new token fused into the
+        # paged-decode launch (msgl_paged_decode_store_planned), then the split-K
+        # merge. One layer per step is bracketed by HIP events (an event record
+        # costs a queue barrier, so recording around every layer would slow the
+        # step down).
+        ops.paged_decode_plan(indptr, None, BATCH, HQ, HKV, D, splits, ws)
         for layer in range(LAYERS):
             if layer == timed_layer:
                 events[0].record()
             ops.paged_decode_attention(qs[layer], kps[layer], vps[layer], indptr, indices, scale,
                                        max_splits=splits, out=outs[layer], workspace=ws,
-                                       new_kv=(ks[layer], vs[layer], out_loc))
+                                       new_kv=(ks[layer], vs[layer], out_loc), planned=True)
             if layer == timed_layer:
                 events[1].record()
 
@@ -237,7 +240,8 @@ def bench_decode(args, dev):
             "workload": (
                 "paged decode, Qwen3-0.6B attention (16 q / 8 kv heads, head_dim 128), 28 layers; batch 128, "
                 "context U[200,2048] (seed 0), page_size 1, 262144-slot bf16 pool per layer, random slots; "
-                "per layer: KV store of the new token + paged decode (one fused launch) + split-K merge"
+                "per step: one decode work-list plan; per layer: KV store of the new token + paged decode (one fused "
+                "launch) + split-K merge"
             ),
             "batch": BATCH,
             "sum_context": int(c.lens.sum()),

@@ -14,6 +14,7 @@
  *   msgl_paged_decode        attention/metal.py:112-131   paged_decode_attention
  *                            (semantics of attention/naive.py:50-60 forward_decode)
  *   msgl_paged_decode_store  kvcache/pool.py:47-50 + attention/metal.py:112-131 in one launch
+ *                            (+ _plan / _planned / _store_planned: plan once per step)
  *   msgl_prefill_ragged      attention/base.py:85-105     BaseAttnBackend._forward_prefill
  *                            (+ _default_splits, _workspace_size)
  *   msgl_build_step_indices  scheduler/scheduler.py:154-157 + attention/metal.py:145-152
@@ -138,6 +139,33 @@ int32_t msgl_prefill_default_splits(int32_t num_reqs, int32_t num_qo_heads, int3
  * row. 0 for invalid sizes. */
 int64_t msgl_prefill_workspace_size(int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
                                     int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t max_splits);
+
+/*
+ * Plan/run split of the decode calls above, for callers that run many layers
+ * over the same indices (one decode step of a model):
+ * msgl_paged_decode_plan writes the work list of (request, chunk) items for
+ * (kv_indptr, seq_lens, batch, heads, max_splits) into the workspace;
+ * msgl_paged_decode_planned / msgl_paged_decode_store_planned take the same
+ * arguments as msgl_paged_decode / msgl_paged_decode_store and use that plan
+ * instead of building it (one launch fewer per call). The plan must have been
+ * built on the same stream, for the same index data, workspace and sizes, and
+ * the workspace must not be re-planned before the calls that use it. No
+ * reference counterpart (MLX decodes layer by layer, attention/metal.py:112-131).
+ */
+int msgl_paged_decode_plan(const int32_t* kv_indptr, const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                           int32_t num_kv_heads, int32_t head_dim, int32_t max_splits, void* workspace,
+                           int64_t workspace_bytes, void* stream);
+int msgl_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool, const int32_t* kv_indptr,
+                              const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                              int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                              int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
+                              void* workspace, int64_t workspace_bytes, void* stream);
+int msgl_paged_decode_store_planned(const void* q, const void* k_new, const void* v_new, const int32_t* out_loc,
+                                    void* k_pool, void* v_pool, const int32_t* kv_indptr, const int32_t* kv_indices,
+                                    const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                                    int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                                    int64_t workspace_bytes, void* stream);
 
 /*
  * Ragged chunked-prefill attention over a paged pool, one launch per batch.

@@ -10,8 +10,11 @@
 //    finishes; the kv heads of one (b, s) are neighbouring workgroups, so the
 //    rows of a slot (Hkv * D contiguous elements) are read close in time. A
 //    workgroup gathers its token slots once into LDS.
-//  * Split-K: request b is cut into n_b <= max_splits chunks of a multiple of
-//    16 tokens (>= kMinChunk), decided on the device from L_b alone. A
+//  * Split-K: every request is cut into chunks of one batch-wide length,
+//    ceil(max_b L_b / max_splits) rounded to 16 tokens (>= kMinChunk), so a
+//    workgroup never gathers more than one chunk; a one-workgroup plan kernel
+//    lists the (request, chunk, kv-head group) items longest first, so the
+//    grid has no empty workgroups and the long items start first. A
 //    single-chunk request writes its final row. Otherwise every chunk writes
 //    fp32 partials (acc, m, l) and a merge kernel with one wavefront per
 //    (request, kv head) combines them. Merging inside the decode launch was
@@ -85,18 +88,18 @@ struct QK<float> {
   }
 };
 
-// Split geometry of one request.
-__device__ __forceinline__ void split_geometry(int L, int max_splits, int& n, int& chunk) {
+// Split geometry of one request: chunks of the batch-wide length chunk_len
+// (the plan kernel's ceil(max_b L_b / max_splits), a multiple of 16 tokens),
+// at most max_splits of them, the last one taking the rest. Used identically
+// by the plan, decode and merge kernels.
+__device__ __forceinline__ void split_geometry(int L, int max_splits, int chunk_len, int& n, int& chunk) {
   if (L <= 0) {
     n = 0;
     chunk = 0;
     return;
   }
-  int want = (L + kMinChunk - 1) / kMinChunk;
-  if (want > max_splits) want = max_splits;
-  chunk = (L + want - 1) / want;
-  chunk = (chunk + 15) & ~15;
-  n = (L + chunk - 1) / chunk;
+  chunk = chunk_len;
+  n = min(max_splits, (L + chunk - 1) / chunk);
 }
 
 __device__ __forceinline__ int slot_of(const int32_t* __restrict__ kv_indices, int start, int tok, int page_size,
@@ -126,8 +129,12 @@ struct DecodeParams {
   const int32_t* out_loc;  // [B] slot of each request's newest token (position L_b - 1)
   void* k_pool_w;
   void* v_pool_w;
+  // work list (plan kernel output, in the workspace)
+  int* meta;        // [0] items in the plan, [1] batch-wide chunk length
+  int4* plan;       // (request, split, kv-head group, 0), longest first
   int64_t num_slots;
-  int hq, hkv, page_size, max_splits;
+  int hq, hkv, page_size, max_splits, batch, ngrp;
+  bool planned;  // the workspace already holds this call's plan
   float scale_log2;
 };
 
@@ -186,15 +193,17 @@ void paged_decode_kernel(DecodeParams p) {
   float* ML_lds = lds + 256 + 16;  // [16][2]
   uint8_t* K_lds = reinterpret_cast<uint8_t*>(lds + kLdsPerWave);  // [16][KRS bytes]
 
-  // grid.x = split * kv-head groups + group; a group is this workgroup's waves
-  const int ngrp = (p.hkv + nwaves - 1) / nwaves;
-  const int b = blockIdx.y;
-  const int split = blockIdx.x / ngrp;
-  const int kgrp = blockIdx.x % ngrp;
+  // work item from the plan (workgroups past its end have nothing to do); a
+  // kv-head group is this workgroup's waves
+  if ((int)blockIdx.x >= p.meta[0]) return;
+  const int4 item = p.plan[blockIdx.x];
+  const int b = item.x;
+  const int split = item.y;
+  const int kgrp = item.z;
   const int start = p.kv_indptr[b];
   const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - start;
   int n, chunk;
-  split_geometry(L, p.max_splits, n, chunk);
+  split_geometry(L, p.max_splits, p.meta[1], n, chunk);
   if (split >= n) {
     if (split == 0) {  // L == 0: defined zero output for this group's heads
       const int h0 = kgrp * nwaves * G;
@@ -205,7 +214,7 @@ void paged_decode_kernel(DecodeParams p) {
     return;
   }
   const int t0 = split * chunk;
-  const int t1 = min(L, t0 + chunk);
+  const int t1 = split == n - 1 ? L : t0 + chunk;
 
   const int r = lane & 15;    // MFMA column (token in tile) / A row
   const int g4 = lane >> 4;   // MFMA row group
@@ -424,7 +433,7 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p,
   const int b = unit / p.hkv, kvh = unit % p.hkv;
   const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];
   int n, chunk;
-  split_geometry(L, p.max_splits, n, chunk);
+  split_geometry(L, p.max_splits, p.meta[1], n, chunk);
   if (n <= 1) return;
   const int64_t bbase = (int64_t)b * p.max_splits * p.hq + kvh * G;
   constexpr int C4 = D / 4;
@@ -481,14 +490,93 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p,
 #define MSGL_DECODE_WAVES_PER_WG 4
 #endif
 
+// Work list for paged_decode_kernel, one workgroup: the batch-wide chunk length
+// ceil(max_b L_b / max_splits) (a multiple of 16, >= kMinChunk), then every
+// (request, chunk) counting-sorted by its 16-token tile count, longest first,
+// each expanded to the kv-head groups as consecutive items. Every workgroup
+// then gathers at most one chunk, the long ones are dispatched first and no
+// empty workgroup sits between real ones; a request with L = 0 keeps its
+// (zero-output) chunk 0. The order does not change any result.
+constexpr int kPlanThreads = 1024;
+
+constexpr int kPlanLds = 8192;  // request lengths staged in LDS (larger batches read them again)
+
+__device__ __forceinline__ int decode_item_tiles(int L, int max_splits, int split, int chunk_len) {
+  if (L <= 0) return split == 0 ? 1 : 0;
+  int n, chunk;
+  split_geometry(L, max_splits, chunk_len, n, chunk);
+  if (split >= n) return 0;
+  const int len = split == n - 1 ? L - split * chunk : chunk;
+  return (len + 15) / 16;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeParams p) {
+  __shared__ int lens[kPlanLds];
+  __shared__ int hist[256];
+  __shared__ int wmax[kPlanThreads / 64];
+  __shared__ int chunk_s;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const bool staged = p.batch <= kPlanLds;
+  auto len_of = [&](int b) {
+    return staged ? lens[b] : (p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b]);
+  };
+  int m = 0;
+  for (int b = threadIdx.x; b < p.batch; b += kPlanThreads) {
+    const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];
+    if (staged) lens[b] = L;
+    m = max(m, L);
+  }
+  for (int d = 32; d >= 1; d >>= 1) m = max(m, __shfl_xor(m, d));
+  if (lane == 0) wmax[wave] = m;
+  for (int i = threadIdx.x; i < 256; i += kPlanThreads) hist[i] = 0;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    int mx = 0;
+    for (int w = 0; w < kPlanThreads / 64; ++w) mx = max(mx, wmax[w]);
+    int c = (mx + p.max_splits - 1) / p.max_splits;
+    c = max(kMinChunk, (c + 15) & ~15);
+    chunk_s = c;
+    p.meta[1] = c;
+  }
+  __syncthreads();
+  const int chunk_len = chunk_s;
+  const int ncand = p.batch * p.max_splits;
+  for (int t = threadIdx.x; t < ncand; t += kPlanThreads) {
+    const int n = decode_item_tiles(len_of(t / p.max_splits), p.max_splits, t % p.max_splits, chunk_len);
+    if (n > 0) atomicAdd(&hist[min(n, 255)], 1);
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {  // exclusive offsets, longest bucket first
+    int run = 0;
+    for (int i = 255; i >= 1; --i) {
+      const int c = hist[i];
+      hist[i] = run;
+      run += c;
+    }
+    p.meta[0] = run * p.ngrp;
+  }
+  __syncthreads();
+  for (int t = threadIdx.x; t < ncand; t += kPlanThreads) {
+    const int b = t / p.max_splits, split = t % p.max_splits;
+    const int n = decode_item_tiles(len_of(b), p.max_splits, split, chunk_len);
+    if (n > 0) {
+      const int pos = atomicAdd(&hist[min(n, 255)], 1);
+      for (int g = 0; g < p.ngrp; ++g) p.plan[pos * p.ngrp + g] = make_int4(b, split, g, 0);
+    }
+  }
+}
+
 template <typename T, int D, int G>
 static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
   const int nwaves = p.hkv < MSGL_DECODE_WAVES_PER_WG ? p.hkv : MSGL_DECODE_WAVES_PER_WG;
-  const int ngrp = (p.hkv + nwaves - 1) / nwaves;
   const size_t lds = ((size_t)kSeg + kSlotPad + (size_t)nwaves * (kLdsPerWave + 16 * k_lds_stride<T, D>() / 4)) *
                      sizeof(float);
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, G>), dim3(p.max_splits * ngrp, batch), dim3(64 * nwaves), lds, stream,
-                     p);
+  if (!p.planned) {
+    hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
+    MSGL_CHECK_LAUNCH("msgl_paged_decode (plan)");
+  }
+  hipLaunchKernelGGL((paged_decode_kernel<T, D, G>), dim3(batch * p.max_splits * p.ngrp), dim3(64 * nwaves), lds,
+                     stream, p);
   MSGL_CHECK_LAUNCH("msgl_paged_decode");
   if (p.max_splits > 1) {
     const int units = batch * p.hkv;
@@ -524,8 +612,27 @@ static int dispatch_dim(const DecodeParams& p, int batch, int head_dim, int grou
   }
 }
 
-// Workspace layout: [m,l B*S*Hq*2 f32 | acc B*S*Hq*D f32], each region 256-byte aligned.
+// Workspace layout, each region 256-byte aligned: [meta | plan B*S*ngrp int4 |
+// (S > 1) m,l B*S*Hq*2 f32 | acc B*S*Hq*D f32].
 static inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+static inline int decode_groups(int hkv) {
+  const int nwaves = hkv < MSGL_DECODE_WAVES_PER_WG ? hkv : MSGL_DECODE_WAVES_PER_WG;
+  return (hkv + nwaves - 1) / nwaves;
+}
+
+struct DecodeWorkspace {
+  int64_t plan, part_ml, part_o, bytes;
+};
+static inline DecodeWorkspace decode_workspace(int batch, int hq, int hkv, int head_dim, int splits) {
+  DecodeWorkspace w;
+  const int64_t units = splits > 1 ? (int64_t)batch * splits * hq : 0;
+  w.plan = 256;
+  w.part_ml = w.plan + align256((int64_t)batch * splits * decode_groups(hkv) * 16);
+  w.part_o = w.part_ml + align256(units * 2 * 4);
+  w.bytes = w.part_o + align256(units * head_dim * 4);
+  return w;
+}
 
 }  // namespace msgl
 
@@ -547,15 +654,15 @@ extern "C" int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_k
 
 extern "C" int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
                                                     int32_t head_dim, int32_t max_splits) {
-  using msgl::align256;
   if (batch <= 0 || num_qo_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0) return 0;
   if (max_splits > msgl::kMaxSplits) max_splits = msgl::kMaxSplits;
-  if (max_splits <= 1) return 0;
-  const int64_t units = (int64_t)batch * max_splits * num_qo_heads;
-  return align256(units * 2 * 4) + align256(units * head_dim * 4);
+  if (max_splits < 1) max_splits = 1;
+  return msgl::decode_workspace(batch, num_qo_heads, num_kv_heads, head_dim, max_splits).bytes;
 }
 
-static int paged_decode_impl(const char* fn, const void* q, const void* k_new, const void* v_new,
+enum DecodeMode { kPlanAndRun, kRunPlanned };
+
+static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, const void* k_new, const void* v_new,
                              const int32_t* out_loc, const void* k_pool, const void* v_pool,
                              const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
                              int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
@@ -567,9 +674,55 @@ extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* 
                                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                  int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                                  void* workspace, int64_t workspace_bytes, void* stream) {
-  return paged_decode_impl("msgl_paged_decode", q, nullptr, nullptr, nullptr, k_pool, v_pool, kv_indptr, kv_indices,
-                           seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size, num_slots, dtype, scale,
-                           max_splits, out, workspace, workspace_bytes, stream);
+  return paged_decode_impl("msgl_paged_decode", kPlanAndRun, q, nullptr, nullptr, nullptr, k_pool, v_pool, kv_indptr,
+                           kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size, num_slots,
+                           dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int msgl_paged_decode_plan(const int32_t* kv_indptr, const int32_t* seq_lens, int32_t batch,
+                                      int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                      int32_t max_splits, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(batch >= 0 && batch <= 65535, "msgl_paged_decode_plan: batch must be in [0, 65535]");
+  if (batch == 0) return MSGL_OK;
+  MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0 && num_qo_heads % num_kv_heads == 0,
+                 "msgl_paged_decode_plan: bad head counts");
+  MSGL_CHECK_ARG(kv_indptr != nullptr, "msgl_paged_decode_plan: null kv_indptr");
+  if (max_splits <= 0) max_splits = msgl_paged_decode_default_splits(batch, num_kv_heads, 0);
+  if (max_splits > kMaxSplits) max_splits = kMaxSplits;
+  const int64_t need = msgl_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
+  if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0) {
+    set_error("msgl_paged_decode_plan: 256-byte aligned workspace of %lld bytes needed, %lld given",
+              (long long)need, (long long)workspace_bytes);
+    return MSGL_ERR_WORKSPACE;
+  }
+  DecodeParams p{};
+  const DecodeWorkspace w = decode_workspace(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  p.kv_indptr = kv_indptr;
+  p.seq_lens = seq_lens;
+  p.meta = reinterpret_cast<int*>(ws);
+  p.plan = reinterpret_cast<int4*>(ws + w.plan);
+  p.hq = num_qo_heads;
+  p.hkv = num_kv_heads;
+  p.max_splits = max_splits;
+  p.batch = batch;
+  p.ngrp = decode_groups(num_kv_heads);
+  hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, p);
+  MSGL_CHECK_LAUNCH("msgl_paged_decode_plan");
+  return MSGL_OK;
+}
+
+extern "C" int msgl_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool,
+                                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                                         const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                         int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                                         int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                                         int64_t workspace_bytes, void* stream) {
+  return paged_decode_impl("msgl_paged_decode_planned", kRunPlanned, q, nullptr, nullptr, nullptr, k_pool, v_pool,
+                           kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
+                           num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
 }
 
 extern "C" int msgl_paged_decode_store(const void* q, const void* k_new, const void* v_new, const int32_t* out_loc,
@@ -584,12 +737,29 @@ extern "C" int msgl_paged_decode_store(const void* q, const void* k_new, const v
   MSGL_CHECK_ARG(k_new && v_new && out_loc, "msgl_paged_decode_store: null k_new, v_new or out_loc");
   MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
                  "msgl_paged_decode_store: k_new and v_new must be 16-byte aligned");
-  return paged_decode_impl("msgl_paged_decode_store", q, k_new, v_new, out_loc, k_pool, v_pool, kv_indptr,
-                           kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size, num_slots,
-                           dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
+  return paged_decode_impl("msgl_paged_decode_store", kPlanAndRun, q, k_new, v_new, out_loc, k_pool, v_pool,
+                           kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
+                           num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
 }
 
-static int paged_decode_impl(const char* fn, const void* q, const void* k_new, const void* v_new,
+extern "C" int msgl_paged_decode_store_planned(const void* q, const void* k_new, const void* v_new,
+                                               const int32_t* out_loc, void* k_pool, void* v_pool,
+                                               const int32_t* kv_indptr, const int32_t* kv_indices,
+                                               const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                               int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                               int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                                               void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(k_new && v_new && out_loc, "msgl_paged_decode_store_planned: null k_new, v_new or out_loc");
+  MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
+                 "msgl_paged_decode_store_planned: k_new and v_new must be 16-byte aligned");
+  return paged_decode_impl("msgl_paged_decode_store_planned", kRunPlanned, q, k_new, v_new, out_loc, k_pool, v_pool,
+                           kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
+                           num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
+}
+
+static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, const void* k_new, const void* v_new,
                              const int32_t* out_loc, const void* k_pool, const void* v_pool,
                              const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
                              int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
@@ -617,7 +787,7 @@ static int paged_decode_impl(const char* fn, const void* q, const void* k_new, c
   if (max_splits > kMaxSplits) max_splits = kMaxSplits;
   const int64_t need =
       msgl_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
-  if (need > 0 && (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0)) {
+  if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0) {
     set_error("%s: 256-byte aligned workspace of %lld bytes needed, %lld given", fn, (long long)need,
               (long long)workspace_bytes);
     return MSGL_ERR_WORKSPACE;
@@ -635,10 +805,15 @@ static int paged_decode_impl(const char* fn, const void* q, const void* k_new, c
   p.out_loc = out_loc;
   p.k_pool_w = const_cast<void*>(k_pool);
   p.v_pool_w = const_cast<void*>(v_pool);
-  const int64_t units = (int64_t)batch * max_splits * num_qo_heads;
+  const DecodeWorkspace w = decode_workspace(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
-  p.part_ml = need > 0 ? reinterpret_cast<float*>(ws) : nullptr;
-  p.part_o = need > 0 ? reinterpret_cast<float*>(ws + align256(units * 2 * 4)) : nullptr;
+  p.meta = reinterpret_cast<int*>(ws);
+  p.plan = reinterpret_cast<int4*>(ws + w.plan);
+  p.part_ml = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_ml) : nullptr;
+  p.part_o = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_o) : nullptr;
+  p.batch = batch;
+  p.ngrp = decode_groups(num_kv_heads);
+  p.planned = mode == kRunPlanned;
   p.num_slots = num_slots;
   p.hq = num_qo_heads;
   p.hkv = num_kv_heads;

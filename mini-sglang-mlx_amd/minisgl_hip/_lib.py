@@ -64,6 +64,14 @@ SIGNATURES = {
             _c_i32, _c_p, _c_p, _c_i64, _c_p,  # max_splits, out, workspace, ws_bytes, stream
         ],
     ),
+    "msgl_paged_decode_plan": (
+        ctypes.c_int,
+        [
+            _c_p, _c_p, _c_i32,  # kv_indptr, seq_lens, batch
+            _c_i32, _c_i32, _c_i32, _c_i32,  # Hq, Hkv, D, max_splits
+            _c_p, _c_i64, _c_p,  # workspace, ws_bytes, stream
+        ],
+    ),
     "msgl_prefill_ragged": (
         ctypes.c_int,
         [
@@ -88,6 +96,9 @@ SIGNATURES = {
     "msgl_prefill_default_splits": (_c_i32, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
     "msgl_prefill_workspace_size": (_c_i64, [_c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32]),
 }
+
+SIGNATURES["msgl_paged_decode_planned"] = SIGNATURES["msgl_paged_decode"]
+SIGNATURES["msgl_paged_decode_store_planned"] = SIGNATURES["msgl_paged_decode_store"]
 
 _lib = None
 

@@ -42,6 +42,7 @@ class HipDecodeMetadata:
     kv_indices: torch.Tensor  # [sum L] int32, device
     max_seq_len: int
     max_splits: int
+    workspace: torch.Tensor  # this step's: the decode work list (planned once) and split-K partials
 
 
 @dataclass
@@ -83,18 +84,21 @@ class HipAttnBackend(BaseAttnBackend):
         valid = np.arange(max_len)[None, :] < lens[:, None]
         kv_indices = self.page_table[rows, :max_len][valid]
         kv_indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
-        splits = ops.default_splits(len(lens), self.config.num_kv_heads, max_len)
+        cfg = self.config
+        b = len(lens)
+        splits = ops.default_splits(b, cfg.num_kv_heads, max_len)
+        indptr_dev = _to_device(kv_indptr, self.device)
+        # a workspace per step, so a step prepared while the previous one still
+        # runs (scheduler/scheduler.py:88-118) never touches the running step's plan
+        ws = torch.empty(ops.decode_workspace_bytes(b, cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, splits),
+                         dtype=torch.uint8, device=self.device)
+        ops.paged_decode_plan(indptr_dev, None, b, cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, splits, ws)
         return HipDecodeMetadata(
-            kv_indptr=_to_device(kv_indptr, self.device),
+            kv_indptr=indptr_dev,
             kv_indices=_to_device(kv_indices, self.device),
             max_seq_len=max_len,
             max_splits=splits,
-        )
-
-    def _decode_workspace(self, batch_size: int, max_splits: int) -> Optional[torch.Tensor]:
-        cfg = self.config
-        return self._shared_workspace(
-            ops.decode_workspace_bytes(batch_size, cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, max_splits)
+            workspace=ws,
         )
 
     def _shared_workspace(self, need: int) -> Optional[torch.Tensor]:
@@ -106,7 +110,7 @@ class HipAttnBackend(BaseAttnBackend):
         return self._workspace
 
     def forward_decode(self, q: torch.Tensor, layer_id: int, meta: HipDecodeMetadata) -> torch.Tensor:
-        ws = self._decode_workspace(q.shape[0], meta.max_splits)
+        ws = meta.workspace
         pending = self.kv_cache.take_pending(layer_id) if self.fuse_decode_store else None
         if pending is not None and pending[0].shape[0] != q.shape[0]:
             k, v, out_loc = pending  # not one new token per request: store eagerly
@@ -122,6 +126,7 @@ class HipAttnBackend(BaseAttnBackend):
             max_splits=meta.max_splits,
             workspace=ws,
             new_kv=pending,
+            planned=True,
         )
 
     # ------------------------------------------------------------------ prefill

@@ -102,6 +102,28 @@ def prefill_workspace(num_reqs: int, num_tokens: int, max_extend_len: int, num_q
     return torch.empty(need, dtype=torch.uint8, device=device)
 
 
+def paged_decode_plan(
+    kv_indptr: torch.Tensor,
+    seq_lens: Optional[torch.Tensor],
+    batch: int,
+    num_qo_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    max_splits: int,
+    workspace: torch.Tensor,
+) -> None:
+    """Build the decode work list for these indices into ``workspace`` (reused by
+    every ``paged_decode_attention(..., planned=True)`` call over them)."""
+    dev = workspace.device
+    _check_index("kv_indptr", kv_indptr, dev)
+    _check_index("seq_lens", seq_lens, dev)
+    status = _lib.load().msgl_paged_decode_plan(
+        _lib.ptr(kv_indptr), _lib.ptr(seq_lens), batch, num_qo_heads, num_kv_heads, head_dim, max_splits,
+        _lib.ptr(workspace), workspace.numel() * workspace.element_size(), _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_paged_decode_plan")
+
+
 def paged_decode_attention(
     q: torch.Tensor,
     k_pool: torch.Tensor,
@@ -117,6 +139,7 @@ def paged_decode_attention(
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
     new_kv: Optional[tuple] = None,
+    planned: bool = False,
 ) -> torch.Tensor:
     """Paged decode attention; counterpart of attention/metal.py:112-131.
 
@@ -126,7 +149,9 @@ def paged_decode_attention(
     is allocated per call when not given. With ``new_kv = (k_new, v_new,
     out_loc)`` the KV store of this step's rows (kvcache/pool.py:47-50) runs in
     the same launch: k_pool[out_loc] = k_new, v_pool[out_loc] = v_new, where
-    out_loc[b] is the slot of request b's last position.
+    out_loc[b] is the slot of request b's last position. With ``planned`` the
+    workspace already holds the work list built by ``paged_decode_plan`` for
+    these indices and sizes (one launch fewer per call).
     """
     if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
         raise ValueError("q must be [B, Hq, D] and pools [N, Hkv, D]")
@@ -158,6 +183,8 @@ def paged_decode_attention(
         max_splits = int(lib.msgl_paged_decode_default_splits(b, hkv, max_seq_len))
     need = int(lib.msgl_paged_decode_workspace_size(b, hq, hkv, d, max_splits))
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        if planned:
+            raise ValueError("planned decode needs the workspace its plan was built in")
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     common = (
@@ -166,7 +193,8 @@ def paged_decode_attention(
         max_splits, _lib.ptr(out), _lib.ptr(workspace), ws_bytes, _lib.current_stream(dev),
     )
     if new_kv is None:
-        status = lib.msgl_paged_decode(_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool), *common)
+        fn = lib.msgl_paged_decode_planned if planned else lib.msgl_paged_decode
+        status = fn(_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool), *common)
         _lib.check(status, "msgl_paged_decode")
     else:
         k_new, v_new, out_loc = new_kv
@@ -177,7 +205,8 @@ def paged_decode_attention(
         for name, t in (("k_new", k_new), ("v_new", v_new)):
             _check_device(name, t, dev)
         _check_index("out_loc", out_loc, dev)
-        status = lib.msgl_paged_decode_store(
+        fn = lib.msgl_paged_decode_store_planned if planned else lib.msgl_paged_decode_store
+        status = fn(
             _lib.ptr(q), _lib.ptr(k_new), _lib.ptr(v_new), _lib.ptr(out_loc), _lib.ptr(k_pool), _lib.ptr(v_pool),
             *common,
         )

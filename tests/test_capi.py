@@ -36,11 +36,12 @@ def test_every_declared_symbol_is_exported_and_bound():
 def test_abi_version_and_sizes():
     lib = _lib.load()
     assert lib.msgl_abi_version() == 1
-    assert lib.msgl_paged_decode_workspace_size(128, 16, 8, 128, 1) == 0
+    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
+    # [meta | work list: B x splits x kv-head groups (8 heads / 4 per workgroup) int4 | partials]
+    assert lib.msgl_paged_decode_workspace_size(128, 16, 8, 128, 1) == 256 + up(128 * 1 * 2 * 16)
     ws = lib.msgl_paged_decode_workspace_size(128, 16, 8, 128, 16)
     units = 128 * 16 * 16
-    up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    assert ws == up(units * 8) + up(units * 128 * 4)
+    assert ws == 256 + up(128 * 16 * 2 * 16) + up(units * 8) + up(units * 128 * 4)
     assert lib.msgl_paged_decode_workspace_size(1, 16, 8, 128, 1000) == lib.msgl_paged_decode_workspace_size(
         1, 16, 8, 128, 64)
     assert 1 <= lib.msgl_paged_decode_default_splits(128, 8, 2048) <= 64
@@ -82,8 +83,11 @@ def test_host_side_argument_errors():
     # workspace too small for split-K
     st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 4, 16, 8, 128, 1, 100, 1, 0.1, 8, 16, nul, 0, nul)
     assert st == _lib.MSGL_ERR_WORKSPACE
-    # unsupported head_dim is reported (dispatch happens before any launch)
-    st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 1, 16, 8, 96, 1, 100, 1, 0.1, 1, 16, nul, 0, nul)
+    # every decode needs the work-list workspace
+    st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 4, 16, 8, 128, 1, 100, 1, 0.1, 1, 16, nul, 0, nul)
+    assert st == _lib.MSGL_ERR_WORKSPACE
+    # unsupported head_dim is reported (dispatch happens before any launch; the workspace is never touched)
+    st = lib.msgl_paged_decode(16, 16, 16, 16, 16, nul, 1, 16, 8, 96, 1, 100, 1, 0.1, 1, 16, 256, 1 << 30, nul)
     assert st == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
     # prefill: (q, kp, vp, q_indptr, kv_indptr, kv_indices, seq_lens, R, T, maxE, maxL, Hq, Hkv, D, page, slots,
     #           dtype, scale, splits, out, ws, ws_bytes, stream)

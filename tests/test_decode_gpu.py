@@ -222,3 +222,25 @@ def test_fused_store_matches_two_calls(cuda_device, dtype, splits):
     assert torch.equal(out, ref_out)
     ref = oracle.paged_decode(to_np64(q), to_np64(kp2), to_np64(vp2), c.kv_indptr, c.kv_indices, 128**-0.5)
     assert_close(out, ref, dt, f"fused store {dtype}")
+
+
+@pytest.mark.parametrize("splits", [1, 4, 16])
+def test_planned_matches_unplanned(cuda_device, splits):
+    """A plan built once and reused (msgl_paged_decode_plan + *_planned) gives the
+    same bits as the self-planning calls, across layers with different pools."""
+    c = workloads.decode_case(40, 1, 3000, 1 << 17, 1, seed=9)
+    dt = torch.bfloat16
+    q = randn((40, 16, 128), 901, dt).to(cuda_device)
+    indptr, indices = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    ws = ops.decode_workspace(40, 16, 8, 128, splits, cuda_device)
+    print(f"case planned decode splits={splits}", flush=True)
+    ops.paged_decode_plan(indptr, None, 40, 16, 8, 128, splits, ws)
+    for layer in range(3):
+        kp, vp = _pools(1 << 17, 8, 128, dt, 910 + 2 * layer, cuda_device)
+        a = ops.paged_decode_attention(q, kp, vp, indptr, indices, 128**-0.5, max_splits=splits, workspace=ws,
+                                       planned=True)
+        b = ops.paged_decode_attention(q, kp, vp, indptr, indices, 128**-0.5, max_splits=splits)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"planned != unplanned at layer {layer}"
+    ref = _sampled_ref(q, kp, vp, c, [0, 13, 39], 128**-0.5)
+    assert_close(b[[0, 13, 39]], ref, dt, "planned decode")
