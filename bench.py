@@ -50,7 +50,7 @@ TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_cfg2_traffic.txt"
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "prefill", "mixed"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "prefill", "mixed", "ceilings"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
@@ -136,7 +136,8 @@ def main():
         torch.cuda.synchronize()
         del src, dst
     if args.workload != "decode":
-        line = {"decode8b": bench_decode8b, "prefill": bench_prefill, "mixed": bench_mixed}[args.workload](args, dev)
+        line = {"decode8b": bench_decode8b, "prefill": bench_prefill, "mixed": bench_mixed,
+                "ceilings": bench_ceilings}[args.workload](args, dev)
         print(json.dumps(line), flush=True)
         return
     bench_decode(args, dev)
@@ -455,6 +456,49 @@ def bench_mixed(args, dev):
         {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None},
         higher=False,
+    )
+
+
+def bench_ceilings(args, dev):
+    """The box's own ceilings next to the spec peaks: a 1 GiB device-to-device
+    copy (HBM read + write) and an 8192^3 bf16 GEMM (hipBLASLt via torch)."""
+    import torch
+
+    n = 1 << 30
+    src = torch.empty(n, dtype=torch.uint8, device=dev)
+    dst = torch.empty_like(src)
+
+    def copy(i, ev):
+        if ev:
+            ev[0].record()
+        dst.copy_(src)
+        if ev:
+            ev[1].record()
+
+    sec, ev_s = _timed(args, copy)
+    copy_gbs = 2 * n / ev_s / 1e9
+    del src, dst
+    m = 8192
+    gen = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn((m, m), generator=gen, device=dev, dtype=torch.bfloat16)
+    b = torch.randn((m, m), generator=gen, device=dev, dtype=torch.bfloat16)
+
+    def gemm(i, ev):
+        if ev:
+            ev[0].record()
+        torch.matmul(a, b)
+        if ev:
+            ev[1].record()
+
+    _, gemm_s = _timed(args, gemm)
+    tflops = 2 * m**3 / gemm_s / 1e12
+    return _line(
+        args, "device ceilings: copy GB/s and bf16 GEMM TFLOP/s", copy_gbs, "GB/s", sec * 1e3,
+        "1 GiB device-to-device copy (read + write counted) and an 8192x8192x8192 bf16 GEMM (torch.matmul)",
+        {"copy_gbs": round(copy_gbs, 1), "copy_frac_of_8tbs": round(copy_gbs / HBM_PEAK_GBS, 4),
+         "gemm_tflops": round(tflops, 1), "gemm_frac_of_2500": round(tflops / MFMA_PEAK_TFLOPS, 4)},
+        {"bound": "hbm", "achieved": round(copy_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(copy_gbs / HBM_PEAK_GBS, 4), "traffic": 2 * n},
     )
 
 

@@ -640,12 +640,17 @@ extern "C" int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_k
   // Aim for ~4096 wavefronts (a bit over one round of MI355X at 3 waves/SIMD):
   // enough units for ragged lengths to balance, few enough that the split-K
   // partials and the merge stay small. No chunk is shorter than kMinChunk.
+  // Chunks of at most kMaxChunk tokens keep long-context batches balanced
+  // (the dispatcher needs more items than resident slots).
   if (batch <= 0 || num_kv_heads <= 0) return 1;
+  constexpr int64_t kMaxChunk = 2048;
   const int64_t target_waves = 4096;
   int64_t s = (target_waves + (int64_t)batch * num_kv_heads - 1) / ((int64_t)batch * num_kv_heads);
   if (max_seq_len > 0) {
     const int64_t cap = (max_seq_len + msgl::kMinChunk - 1) / msgl::kMinChunk;
     if (s > cap) s = cap;
+    const int64_t floor_s = (max_seq_len + kMaxChunk - 1) / kMaxChunk;
+    if (s < floor_s) s = floor_s;
   }
   if (s < 1) s = 1;
   if (s > msgl::kMaxSplits) s = msgl::kMaxSplits;

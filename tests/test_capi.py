@@ -48,6 +48,8 @@ def test_abi_version_and_sizes():
     assert lib.msgl_paged_decode_default_splits(1, 8, 32768) == 64
     assert lib.msgl_paged_decode_default_splits(128, 8, 2048) == 4
     assert lib.msgl_paged_decode_default_splits(1, 8, 100) == 2  # capped by ceil(100 / 64)
+    assert lib.msgl_paged_decode_default_splits(128, 8, 32768) == 16  # chunks of at most 2048 tokens
+    assert lib.msgl_paged_decode_default_splits(256, 8, 8192) == 4
 
 
 def test_prefill_sizes():
