@@ -44,7 +44,7 @@ HBM_PEAK_GBS = 8000.0
 METRIC = "paged-decode HBM GB/s (% of peak) + µs/layer at batch 128, Qwen3-0.6B shapes"
 HQ, HKV, D, LAYERS = 16, 8, 128, 28
 BATCH, LO, HI, POOL = 128, 200, 2048, 262144
-TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_cfg2_traffic.txt"
+TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_b128_ctx2k_traffic.txt"
 
 
 def parse_args():
@@ -57,7 +57,7 @@ def parse_args():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
-                    help="first copy 1 GiB device-to-device 3 times (reference kernel for HBM byte counters)")
+                    help="first run y = x * 1 over 1 GiB of fp32 3 times (reference kernel for HBM byte counters)")
     return ap.parse_args()
 
 
@@ -129,10 +129,12 @@ def main():
 
     dev = torch.device("cuda:0")
     if args.copy_calibration:
-        src = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+        # a plain streaming kernel of known traffic for the HBM byte counters:
+        # y = x * 1 over 1 GiB of fp32 (1 GiB read, 1 GiB written), 3 times
+        src = torch.ones((1 << 28,), dtype=torch.float32, device=dev)
         dst = torch.empty_like(src)
         for _ in range(3):
-            dst.copy_(src)
+            torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
     if args.workload != "decode":
@@ -344,7 +346,8 @@ def bench_decode8b(args, dev):
         {"batch": batch, "sum_context": int(c.lens.sum()), "max_splits": splits, "bytes_per_step": nbytes,
          "us_per_layer": round(sec * 1e6, 2)},
         {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": read_traffic(ROOT / "profiles" / "paged_decode_cfg3_traffic.txt")},
+         "frac": round(ach / HBM_PEAK_GBS, 4),
+         "traffic": read_traffic(ROOT / "profiles" / "paged_decode_8b_b256_ctx8k_page16_traffic.txt")},
     )
 
 
@@ -395,7 +398,8 @@ def bench_prefill(args, dev):
          "flops_per_step": flops, "bytes_per_step": nbytes, "tflops": round(tflops, 2),
          "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4)},
         {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-         "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": read_traffic(ROOT / "profiles" / "prefill_cfg4_traffic.txt")},
+         "frac": round(gbs / HBM_PEAK_GBS, 4),
+         "traffic": read_traffic(ROOT / "profiles" / "prefill_ragged_16req_traffic.txt")},
         higher=False,
     )
 
@@ -454,7 +458,8 @@ def bench_mixed(args, dev):
          "store_bytes": store_bytes, "decode_splits": step.decode_splits, "prefill_splits": step.prefill_splits,
          "step_gbs": round(nbytes / sec / 1e9, 2)},
         {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-         "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None},
+         "frac": round(ach / HBM_PEAK_GBS, 4),
+         "traffic": read_traffic(ROOT / "profiles" / "mixed_step_8b_page16_traffic.txt")},
         higher=False,
     )
 
