@@ -24,6 +24,8 @@ Other workloads (one JSON line each, same fields):
   mixed     one continuous-batching step, Qwen3-8B heads, page 16, 8M-slot pool:
             128 decode requests (context U[512, 32768]) + chunks of 1024 over
             prefixes 0 and 8192, indices built on the GPU from the page table
+  rope      rotate-half RoPE of q and k fused with the KV store over the
+            prefill workload's 2040 packed tokens (Qwen3-0.6B heads), 28 layers
 """
 
 import argparse
@@ -50,7 +52,7 @@ TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_b128_ctx2k_traffic.txt"
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "prefill", "mixed", "ceilings"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "prefill", "mixed", "rope", "ceilings"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
@@ -139,7 +141,7 @@ def main():
         del src, dst
     if args.workload != "decode":
         line = {"decode8b": bench_decode8b, "prefill": bench_prefill, "mixed": bench_mixed,
-                "ceilings": bench_ceilings}[args.workload](args, dev)
+                "rope": bench_rope, "ceilings": bench_ceilings}[args.workload](args, dev)
         print(json.dumps(line), flush=True)
         return
     bench_decode(args, dev)
@@ -400,6 +402,81 @@ def bench_prefill(args, dev):
         {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(gbs / HBM_PEAK_GBS, 4),
          "traffic": read_traffic(ROOT / "profiles" / "prefill_ragged_16req_traffic.txt")},
+        higher=False,
+    )
+
+
+def bench_rope(args, dev):
+    """Rotate q and k and store k/v (one launch) for one packed prefill chunk; 28 layers' pools in rotation."""
+    import torch
+
+    from minisgl_hip import ops, workloads
+    from minisgl_hip.layers import rope_inv_freq
+
+    pool = 1 << 17
+    case = workloads.prefill_case(16, 4096, 64, 512, 2048, num_slots=pool, seed=0)
+    t = case.num_tokens
+    pos = np.concatenate([np.arange(p, p + e) for p, e in zip(case.prefix_lens, case.extend_lens)]).astype(np.int32)
+    loc = np.concatenate([case.kv_indices[case.kv_indptr[i] + p: case.kv_indptr[i + 1]]
+                          for i, p in enumerate(case.prefix_lens)]).astype(np.int32)
+    gen = torch.Generator(device=dev).manual_seed(0)
+    kps = [torch.randn((pool, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    vps = [torch.randn((pool, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    qs = [torch.randn((t, HQ, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    ks = [torch.randn((t, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    vs = [torch.randn((t, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    q_out = torch.empty_like(qs[0])
+    posd = torch.from_numpy(pos).to(dev)
+    locd = torch.from_numpy(loc).to(dev)
+    inv = rope_inv_freq(D, 1e6).to(dev)  # Qwen3 rope_theta
+    nbytes = 2 * t * (HQ + 2 * HKV) * D * 2 + 2 * t * 4 + (D // 2) * 4
+
+    def fused(layer):
+        ops.rope_store_kv(qs[layer], ks[layer], vs[layer], posd, locd, kps[layer], vps[layer], inv, D, q_out=q_out)
+
+    k_rot = torch.empty_like(ks[0])
+
+    def unfused(layer):  # the reference's op order as three launches: rope(q), rope(k), store_kv
+        ops.rope(qs[layer], posd, inv, D, out=q_out)
+        ops.rope(ks[layer], posd, inv, D, out=k_rot)
+        ops.store_kv(k_rot, vs[layer], locd, kps[layer], vps[layer])
+
+    def step_time(fn):
+        """One step = the 28 layers' launches back to back: a spin kernel holds the
+        stream while the host enqueues them, so the events see GPU time only
+        (the host wrapper needs longer per call than one launch runs)."""
+        for i in range(args.warmup):
+            for layer in range(LAYERS):
+                fn(layer)
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(args.steps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda._sleep(6_000_000)  # ~3 ms: longer than the host needs to enqueue a step
+            a.record()
+            for layer in range(LAYERS):
+                fn(layer)
+            b.record()
+            torch.cuda.synchronize()
+            times.append(a.elapsed_time(b) / 1e3)
+        return float(np.median(times))
+
+    sec = step_time(fused)
+    sec_unfused = step_time(unfused)
+    per_launch = sec / LAYERS
+    gbs = nbytes / per_launch / 1e9
+    return _line(
+        args, "fused RoPE + KV store µs/layer, 2040 packed prefill tokens, Qwen3-0.6B heads", per_launch * 1e6, "us",
+        sec * 1e3,
+        "rotate-half RoPE of q and k (rope_theta 1e6, rotary_dim 128) fused with the KV store, Qwen3-0.6B "
+        "attention (16 q / 8 kv heads, head_dim 128); the packed tokens of the prefill workload (16 requests, "
+        "2040 tokens, positions prefix + offset, seed 0) stored into 131072-slot bf16 pools; one step = 28 layers "
+        "back to back (median of steps)",
+        {"packed_tokens": t, "layers": LAYERS, "bytes_per_launch": nbytes,
+         "unfused_three_launch_us_per_layer": round(sec_unfused / LAYERS * 1e6, 2)},
+        {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(gbs / HBM_PEAK_GBS, 4),
+         "traffic": read_traffic(ROOT / "profiles" / "rope_store_kv_prefill2040_traffic.txt")},
         higher=False,
     )
 

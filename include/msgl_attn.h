@@ -20,6 +20,8 @@
  *   msgl_build_step_indices  scheduler/scheduler.py:154-157 + attention/metal.py:145-152
  *                            + attention/base.py:70-83 (index metadata, on the GPU)
  *   msgl_table_scatter       device mirror of scheduler/cache.py:53-72's page-table writes
+ *   msgl_rope                layers.py:45-56 (RotaryEmbedding.__call__, rotate-half mx.fast.rope)
+ *   msgl_rope_store_kv       layers.py:107-109 (rotate q and k, then store_kv) in one launch
  *
  * Layouts (identical to the reference, no transposes at the boundary):
  *   q, out   [T, Hq, D]   row-major, dtype `dtype`
@@ -230,6 +232,33 @@ int msgl_build_step_indices(const int32_t* req_to_token, int64_t num_rows, int64
  */
 int msgl_table_scatter(int32_t* req_to_token, int64_t num_rows, int64_t row_stride, const int32_t* rows,
                        const int32_t* cols, const int32_t* values, int64_t n, void* stream);
+
+/*
+ * Rotary position embedding, rotate-half layout (replaces RotaryEmbedding.__call__,
+ * layers.py:45-56: mx.fast.rope(x[T,H,1,D], rotary_dim, traditional=False,
+ * offset=positions)). For pair i < rotary_dim/2 of token t the angle is the
+ * fp32 product positions[t] * inv_freq[i]; element i pairs with i + rotary_dim/2,
+ * elements >= rotary_dim are copied. inv_freq ([rotary_dim/2] fp32, device)
+ * holds the angular frequencies with any scaling folded in: default
+ * base^(-2i/rotary_dim), linear (layers.py:37-38) times 1/factor, llama3 the
+ * reciprocal of _llama3_freqs (layers.py:59-74).
+ *   x, out     [T, H, D]; out may equal x (in place)
+ *   rotary_dim multiple of 8, <= min(D, 256); D multiple of 4, <= 1024
+ */
+int msgl_rope(const void* x, void* out, const int32_t* positions, const float* inv_freq, int64_t num_tokens,
+              int32_t num_heads, int32_t head_dim, int32_t rotary_dim, int32_t dtype, void* stream);
+
+/*
+ * layers.py:107-109 in one launch: q_out = rope(q), k_pool[out_loc[t]] = rope(k[t]),
+ * v_pool[out_loc[t]] = v[t] (kvcache/pool.py:47-50), and k_out = rope(k) when
+ * k_out is not null. q_out may equal q and k_out may equal k. num_qo_heads may
+ * be 0 (q, q_out unused). Rows whose slot lies outside [0, num_slots) are not
+ * stored.
+ */
+int msgl_rope_store_kv(const void* q, const void* k, const void* v, const int32_t* positions,
+                       const int32_t* out_loc, const float* inv_freq, void* q_out, void* k_out, void* k_pool,
+                       void* v_pool, int64_t num_tokens, int32_t num_qo_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int32_t rotary_dim, int64_t num_slots, int32_t dtype, void* stream);
 
 #ifdef __cplusplus
 }

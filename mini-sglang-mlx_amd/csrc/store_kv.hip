@@ -21,12 +21,13 @@ __global__ __launch_bounds__(256) void store_kv_kernel(const uint8_t* __restrict
        i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t t = i / chunks_per_row;
     const int64_t c = i - t * chunks_per_row;
-    const int64_t slot = out_loc[t];
-    if (slot < 0 || slot >= num_slots) continue;  // never write outside the pool
+    // the data loads do not wait for the slot: all three go out together
     const int64_t src = t * row_bytes + c * 16;
-    const int64_t dst = slot * row_bytes + c * 16;
     const u32x4 kv = ld16(k + src);
     const u32x4 vv = ld16(v + src);
+    const int64_t slot = out_loc[t];
+    if (slot < 0 || slot >= num_slots) continue;  // never write outside the pool
+    const int64_t dst = slot * row_bytes + c * 16;
     st16(k_pool + dst, kv);
     st16(v_pool + dst, vv);
   }

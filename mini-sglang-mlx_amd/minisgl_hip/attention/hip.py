@@ -62,6 +62,9 @@ class HipAttnBackend(BaseAttnBackend):
     ``forward_decode`` performs it inside the decode launch (one kernel instead of
     two per layer); results and pool contents are identical to the eager order."""
 
+    # every key and value is read from the pool (prefill included), never from the k/v arguments
+    reads_kv_from_pool = True
+
     def __init__(self, config, kv_cache, page_table: np.ndarray, fuse_decode_store: bool = True) -> None:
         super().__init__(config, kv_cache, page_table)
         self.device = kv_cache.k[0].device

@@ -111,3 +111,14 @@ class ModelConfig:
     num_kv_heads: int
     head_dim: int
     num_layers: int = 1
+
+
+@dataclass(frozen=True)
+class RotaryConfig:
+    """models/config.py:9-15: rotary_dim = head_dim * partial_rotary_factor, rope_theta, rope_scaling."""
+
+    head_dim: int
+    rotary_dim: int
+    base: float
+    max_position: int = 4096
+    scaling: Optional[dict] = None

@@ -62,6 +62,17 @@ class MHAKVCache:
         else:
             ops.store_kv(k, v, out_loc, self.k[layer_id], self.v[layer_id])
 
+    def rope_store_kv(self, q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, positions: torch.Tensor,
+                      out_loc: torch.Tensor, layer_id: int, rotary, k_out: Optional[torch.Tensor] = None,
+                      q_out: Optional[torch.Tensor] = None) -> torch.Tensor:
+        """layers.py:107-109 fused: rotate q and k, store rotated k and raw v; returns rotated q.
+
+        ``rotary`` carries ``inv_freq`` and ``dims`` (a ``layers.RotaryEmbedding``).
+        The store happens now, whatever ``defer_stores`` says."""
+        self.flush(layer_id)
+        return ops.rope_store_kv(q, k, v, positions, out_loc, self.k[layer_id], self.v[layer_id], rotary.inv_freq,
+                                 rotary.dims, q_out=q_out, k_out=k_out)
+
     def take_pending(self, layer_id: int) -> Optional[PendingStore]:
         """Hand a recorded store to the caller, who becomes responsible for performing it."""
         pending, self._pending[layer_id] = self._pending[layer_id], None

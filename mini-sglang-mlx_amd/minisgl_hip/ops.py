@@ -355,3 +355,83 @@ def table_scatter(req_to_token: torch.Tensor, rows: torch.Tensor, cols: torch.Te
         _lib.ptr(values), n, _lib.current_stream(dev),
     )
     _lib.check(status, "msgl_table_scatter")
+
+
+def _check_rope(inv_freq: torch.Tensor, positions: torch.Tensor, rotary_dim: int, t: int, dev: torch.device) -> None:
+    if inv_freq.dtype != torch.float32 or inv_freq.shape != (rotary_dim // 2,):
+        raise ValueError(f"inv_freq must be float32 [rotary_dim / 2] = [{rotary_dim // 2}]")
+    _check_device("inv_freq", inv_freq, dev)
+    if positions.shape != (t,):
+        raise ValueError("positions must be [T]")
+    _check_index("positions", positions, dev)
+
+
+def rope(
+    x: torch.Tensor, positions: torch.Tensor, inv_freq: torch.Tensor, rotary_dim: int,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """Rotate-half RoPE of x [T, H, D] at per-token positions (layers.py:45-56).
+
+    ``out`` may be ``x`` (in place); inv_freq is [rotary_dim / 2] float32."""
+    if x.dim() != 3:
+        raise ValueError(f"x must be [T, H, D] (got {tuple(x.shape)})")
+    dev = x.device
+    _check_device("x", x, dev)
+    _check_rope(inv_freq, positions, rotary_dim, x.shape[0], dev)
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != x.dtype:
+        raise ValueError("out must match x")
+    _check_device("out", out, dev)
+    status = _lib.load().msgl_rope(
+        _lib.ptr(x), _lib.ptr(out), _lib.ptr(positions), _lib.ptr(inv_freq), x.shape[0], x.shape[1], x.shape[2],
+        rotary_dim, _lib.dtype_code(x.dtype), _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_rope")
+    return out
+
+
+def rope_store_kv(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    positions: torch.Tensor,
+    out_loc: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    inv_freq: torch.Tensor,
+    rotary_dim: int,
+    q_out: Optional[torch.Tensor] = None,
+    k_out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """layers.py:107-109 in one launch: rotate q and k, store rotated k and raw v
+    at out_loc. Returns the rotated q (``q_out``, which may be ``q``); rotated k
+    is also written to ``k_out`` when given (it may be ``k``)."""
+    if q.dim() != 3 or k.dim() != 3 or k.shape != v.shape or q.shape[0] != k.shape[0] or q.shape[2] != k.shape[2]:
+        raise ValueError(f"q must be [T, Hq, D], k/v [T, Hkv, D] (got {tuple(q.shape)}, {tuple(k.shape)})")
+    if k_pool.dim() != 3 or k_pool.shape != v_pool.shape or k_pool.shape[1:] != k.shape[1:]:
+        raise ValueError(f"pools must be [N, Hkv, D] matching k (got {tuple(k_pool.shape)})")
+    if out_loc.shape != (k.shape[0],):
+        raise ValueError("out_loc must be [T]")
+    if len({q.dtype, k.dtype, v.dtype, k_pool.dtype, v_pool.dtype}) != 1:
+        raise ValueError("q, k, v and pools must share one dtype")
+    dev = k_pool.device
+    if q_out is None:
+        q_out = torch.empty_like(q)
+    for name, t in (("q", q), ("k", k), ("v", v), ("k_pool", k_pool), ("v_pool", v_pool), ("q_out", q_out)):
+        _check_device(name, t, dev)
+    if q_out.shape != q.shape or q_out.dtype != q.dtype:
+        raise ValueError("q_out must match q")
+    if k_out is not None:
+        _check_device("k_out", k_out, dev)
+        if k_out.shape != k.shape or k_out.dtype != k.dtype:
+            raise ValueError("k_out must match k")
+    _check_index("out_loc", out_loc, dev)
+    _check_rope(inv_freq, positions, rotary_dim, q.shape[0], dev)
+    status = _lib.load().msgl_rope_store_kv(
+        _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(positions), _lib.ptr(out_loc), _lib.ptr(inv_freq),
+        _lib.ptr(q_out), _lib.ptr(k_out), _lib.ptr(k_pool), _lib.ptr(v_pool), q.shape[0], q.shape[1], k.shape[1],
+        q.shape[2], rotary_dim, k_pool.shape[0], _lib.dtype_code(q.dtype), _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_rope_store_kv")
+    return q_out

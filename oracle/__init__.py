@@ -13,13 +13,16 @@ It restates, in numpy, the reference's algorithm for the attention path
   ``attention/metal.py:145-152``, ``attention/base.py:70-83``;
 - KV store (bit-exact copy): ``kvcache/pool.py:47-50``;
 - attention (fp64 accumulation): ``attention/naive.py:50-60`` (decode),
-  ``attention/base.py:85-105`` (prefill, bottom-right causal).
+  ``attention/base.py:85-105`` (prefill, bottom-right causal);
+- rotary embedding and the rotate-then-store order: ``layers.py:19-74, 107-109``
+  (``rope.py``).
 
 Every function is pinned by a check in ``tests/test_oracle.py`` that does not
 retype its formula: closed forms (one key gives that key's value row, equal
 keys give the mean of the values), brute-force Python loops on tiny inputs,
 an independent library routine (``torch.nn.functional.scaled_dot_product_attention``
-on the CPU), the reference test's fixture construction
+on the CPU), the rotary embedding of ``transformers`` (``apply_rotary_pos_emb`` and its
+llama3 / linear frequency initialisers), the reference test's fixture construction
 (``tests/test_attention.py:19-39``) and the page-layout assertion of
 ``tests/test_cache_manager.py:66-75``, plus mutation tests that plant a
 mistake in a copy of the oracle and show the checks catch it.
@@ -40,4 +43,12 @@ from .attention import (  # noqa: F401
     prepare_batch_indices,
     sdpa,
     store_kv,
+)
+from .rope import (  # noqa: F401
+    rope,
+    rope_angles,
+    rope_inv_freq,
+    rope_periods,
+    rope_position_scale,
+    rope_store_kv,
 )

@@ -117,6 +117,24 @@ def test_host_side_argument_errors():
     assert bi(2, kv_out=nul) == _lib.MSGL_ERR_INVALID
     assert lib.msgl_table_scatter(nul, 4, 64, nul, nul, nul, 0, nul) == _lib.MSGL_OK
     assert lib.msgl_table_scatter(16, 4, 64, nul, 16, 16, 3, nul) == _lib.MSGL_ERR_INVALID
+    # rope: (x, out, positions, inv_freq, T, H, D, rotary_dim, dtype, stream)
+    rp = lambda t=4, h=2, d=128, rot=128, dtype=1, x=16, pos=16: lib.msgl_rope(  # noqa: E731
+        x, x, pos, 16, t, h, d, rot, dtype, nul)
+    assert rp(t=0) == _lib.MSGL_OK
+    assert rp(rot=12) == _lib.MSGL_ERR_INVALID and "rotary_dim" in _lib.last_error()
+    assert rp(rot=136, d=128) == _lib.MSGL_ERR_INVALID
+    assert rp(d=130, rot=64) == _lib.MSGL_ERR_INVALID and "head_dim" in _lib.last_error()
+    assert rp(dtype=5) == _lib.MSGL_ERR_UNSUPPORTED
+    assert rp(pos=nul) == _lib.MSGL_ERR_INVALID and "positions" in _lib.last_error()
+    assert rp(x=8, dtype=0) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
+    # rope_store_kv: (q, k, v, positions, out_loc, inv_freq, q_out, k_out, k_pool, v_pool, T, Hq, Hkv, D, rot,
+    #                 slots, dtype, stream)
+    rs = lambda loc=16, kp=16, slots=100, hkv=8: lib.msgl_rope_store_kv(  # noqa: E731
+        16, 16, 16, 16, loc, 16, 16, nul, kp, 16, 4, 16, hkv, 128, 128, slots, 1, nul)
+    assert rs(loc=nul) == _lib.MSGL_ERR_INVALID and "out_loc" in _lib.last_error()
+    assert rs(kp=nul) == _lib.MSGL_ERR_INVALID and "pools" in _lib.last_error()
+    assert rs(slots=0) == _lib.MSGL_ERR_INVALID
+    assert rs(hkv=0) == _lib.MSGL_ERR_INVALID
     # store_kv: zero tokens is a no-op; bad row size is unsupported
     assert lib.msgl_store_kv(nul, nul, nul, nul, nul, 0, 8, 128, 10, 1, nul) == _lib.MSGL_OK
     assert lib.msgl_store_kv(16, 16, 16, 16, 16, 4, 1, 3, 10, 1, nul) == _lib.MSGL_ERR_UNSUPPORTED
