@@ -24,6 +24,8 @@ Other workloads (one JSON line each, same fields):
   mixed     one continuous-batching step, Qwen3-8B heads, page 16, 8M-slot pool:
             128 decode requests (context U[512, 32768]) + chunks of 1024 over
             prefixes 0 and 8192, indices built on the GPU from the page table
+  decode_fp8  the default decode workload over fp8 e4m3 pools with one scale
+            per slot and kv head (quantising store + fp8 decode per layer)
   rope      rotate-half RoPE of q and k fused with the KV store over the
             prefill workload's 2040 packed tokens (Qwen3-0.6B heads), 28 layers
 """
@@ -52,7 +54,7 @@ TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_b128_ctx2k_traffic.txt"
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "prefill", "mixed", "rope", "ceilings"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "decode_fp8", "prefill", "mixed", "rope", "ceilings"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
@@ -141,7 +143,7 @@ def main():
         del src, dst
     if args.workload != "decode":
         line = {"decode8b": bench_decode8b, "prefill": bench_prefill, "mixed": bench_mixed,
-                "rope": bench_rope, "ceilings": bench_ceilings}[args.workload](args, dev)
+                "rope": bench_rope, "decode_fp8": bench_decode_fp8, "ceilings": bench_ceilings}[args.workload](args, dev)
         print(json.dumps(line), flush=True)
         return
     bench_decode(args, dev)
@@ -267,6 +269,76 @@ def bench_decode(args, dev):
         "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
+
+
+def bench_decode_fp8(args, dev):
+    """The headline decode over fp8 e4m3 pools (one scale per slot and kv head), 28 layers."""
+    import torch
+
+    from minisgl_hip import ops, workloads
+
+    c = workloads.decode_case(BATCH, LO, HI, POOL, 1, seed=0)
+    sum_l = int(c.lens.sum())
+    dec_bytes = sum_l * HKV * (D + 4) * 2 + BATCH * HQ * D * 2 * 2 + sum_l * 4 + (BATCH + 1) * 4
+    store_bytes = BATCH * HKV * (D * 2 * 2 + (D + 4) * 2)  # bf16 rows read, codes + scales written
+    fp8 = torch.float8_e4m3fn
+    gen = torch.Generator(device=dev).manual_seed(0)
+    all_slots = torch.arange(POOL, dtype=torch.int32, device=dev)
+    pools = []
+    for _ in range(LAYERS):  # each layer's pool quantised from N(0,1) bf16 rows
+        kp = torch.empty((POOL, HKV, D), dtype=fp8, device=dev)
+        vp = torch.empty_like(kp)
+        sc = torch.empty((POOL, HKV, 2), dtype=torch.float32, device=dev)
+        src_k = torch.randn((POOL, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        src_v = torch.randn((POOL, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        ops.store_kv_fp8(src_k, src_v, all_slots, kp, vp, sc)
+        pools.append((kp, vp, sc))
+        del src_k, src_v
+    torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    qs = [torch.randn((BATCH, HQ, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    ks = [torch.randn((BATCH, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    vs = [torch.randn((BATCH, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    outs = [torch.empty_like(q) for q in qs]
+    indptr = torch.from_numpy(c.kv_indptr).to(dev)
+    indices = torch.from_numpy(c.kv_indices).to(dev)
+    out_loc = torch.from_numpy(c.out_loc).to(dev)
+    splits = args.splits or ops.default_splits(BATCH, HKV, int(c.lens.max()))
+    ws = ops.decode_workspace(BATCH, HQ, HKV, D, splits, dev)
+
+    def run(i, ev):
+        # per step: one plan; per layer: quantising store of the new token, then fp8 decode + merge
+        ops.paged_decode_plan(indptr, None, BATCH, HQ, HKV, D, splits, ws)
+        timed = i % LAYERS
+        for layer in range(LAYERS):
+            kp, vp, sc = pools[layer]
+            if ev and layer == timed:
+                ev[0].record()
+            ops.store_kv_fp8(ks[layer], vs[layer], out_loc, kp, vp, sc)
+            ops.paged_decode_attention(qs[layer], kp, vp, indptr, indices, D**-0.5, max_splits=splits,
+                                       out=outs[layer], workspace=ws, planned=True, kv_scale=sc)
+            if ev and layer == timed:
+                ev[1].record()
+
+    sec, ev_s = _timed(args, run)
+    step_bytes = LAYERS * (dec_bytes + store_bytes)
+    achieved = (dec_bytes + store_bytes) / ev_s / 1e9
+    line = _line(
+        args, "paged-decode HBM GB/s over an fp8 KV cache, batch 128, Qwen3-0.6B shapes", step_bytes / sec / 1e9,
+        "GB/s", sec * 1e3,
+        "paged decode over fp8 e4m3 pools (one fp32 scale per slot and kv head), Qwen3-0.6B attention (16 q / 8 kv "
+        "heads, head_dim 128), 28 layers; batch 128, context U[200,2048] (seed 0), page_size 1, 262144-slot pools "
+        "quantised from N(0,1) bf16 rows, random slots; per step: one plan; per layer: quantising store of the new "
+        "token + fp8 paged decode + split-K merge",
+        {"batch": BATCH, "sum_context": sum_l, "layers": LAYERS, "max_splits": splits,
+         "bytes_per_layer": dec_bytes + store_bytes, "us_per_layer": round(sec * 1e6 / LAYERS, 2),
+         "store_decode_merge_us": round(ev_s * 1e6, 2)},
+        {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(achieved / HBM_PEAK_GBS, 4),
+         "traffic": read_traffic(ROOT / "profiles" / "paged_decode_fp8_b128_ctx2k_traffic.txt")},
+    )
+    line["dtype"] = "fp8 e4m3 KV, bf16 q/out, fp32 accumulation"
+    return line
 
 
 def _timed(args, run, timed_call=None):

@@ -22,6 +22,8 @@
  *   msgl_table_scatter       device mirror of scheduler/cache.py:53-72's page-table writes
  *   msgl_rope                layers.py:45-56 (RotaryEmbedding.__call__, rotate-half mx.fast.rope)
  *   msgl_rope_store_kv       layers.py:107-109 (rotate q and k, then store_kv) in one launch
+ *   msgl_store_kv_fp8,       the fp8 KV cache of docs/09-exercises.md:81-82 (store_kv and paged
+ *   msgl_paged_decode_fp8    decode over pools of e4m3 codes with one scale per slot and kv head)
  *
  * Layouts (identical to the reference, no transposes at the boundary):
  *   q, out   [T, Hq, D]   row-major, dtype `dtype`
@@ -259,6 +261,46 @@ int msgl_rope_store_kv(const void* q, const void* k, const void* v, const int32_
                        const int32_t* out_loc, const float* inv_freq, void* q_out, void* k_out, void* k_pool,
                        void* v_pool, int64_t num_tokens, int32_t num_qo_heads, int32_t num_kv_heads,
                        int32_t head_dim, int32_t rotary_dim, int64_t num_slots, int32_t dtype, void* stream);
+
+/*
+ * fp8 KV cache (docs/09-exercises.md:81-82: the pool stored as fp8 with one
+ * scale per token and head, store_kv and paged decode changed accordingly).
+ * Pools hold OCP fp8 e4m3 codes [num_slots, Hkv, D] (1 byte each) plus fp32
+ * scales kv_scale [num_slots, Hkv, 2] = (K scale, V scale) of each slot and kv
+ * head (adjacent, so decode reads both with one load); a stored element is
+ * x ~ e4m3(code) * scale.
+ *
+ * msgl_store_kv_fp8 replaces kvcache/pool.py:47-50 for such a pool: for each
+ * (token, kv head) row, amax = max |x|, codes = e4m3(x * (448 / amax)) rounded
+ * to nearest even, scale = amax / 448 (all-zero rows: codes 0, scale 0); rows
+ * whose slot is outside [0, num_slots) are skipped. k, v: [T, Hkv, D] of
+ * `dtype` (16-byte aligned); D / (16 / sizeof(dtype)) must be a power of two <= 64.
+ */
+int msgl_store_kv_fp8(const void* k, const void* v, const int32_t* out_loc, void* k_pool, void* v_pool,
+                      float* kv_scale, int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
+                      int32_t dtype, void* stream);
+
+/*
+ * msgl_paged_decode over fp8 pools (attention/metal.py:112-131 semantics over
+ * the dequantised pool): scores use e4m3(code) on the matrix core with the
+ * row's K scale applied to the score, the V scale folds into the softmax
+ * weight. q/out dtype bf16 or fp16; Hq/Hkv in {1, 2, 4, 8}; head_dim 64/128/256.
+ * Same workspace (msgl_paged_decode_workspace_size) and plan
+ * (msgl_paged_decode_plan) as the unquantised decode; the _planned form skips
+ * the plan like msgl_paged_decode_planned. The new token is stored first with
+ * msgl_store_kv_fp8 (there is no fused-store form).
+ */
+int msgl_paged_decode_fp8(const void* q, const void* k_pool, const void* v_pool, const float* kv_scale,
+                          const int32_t* kv_indptr, const int32_t* kv_indices,
+                          const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                          int32_t head_dim, int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                          int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes, void* stream);
+int msgl_paged_decode_fp8_planned(const void* q, const void* k_pool, const void* v_pool, const float* kv_scale,
+                                  const int32_t* kv_indptr, const int32_t* kv_indices,
+                                  const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
+                                  int32_t head_dim, int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                                  int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
+                                  void* stream);
 
 #ifdef __cplusplus
 }

@@ -49,7 +49,14 @@ inline int dtype_size(int32_t dtype) {
 typedef uint16_t bf16_t;  // raw bfloat16 bits
 typedef _Float16 f16_t;
 
+// OCP fp8 e4m3 ("e4m3fn": bias 7, largest finite 448), the KV-cache storage
+// format of the quantised pool; a distinct type so templates can select on it.
+struct fp8e4m3 {
+  uint8_t bits;
+};
+
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
@@ -97,6 +104,22 @@ struct Vec16<f16_t> {
     for (int i = 0; i < 4; ++i) {
       out[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r[i] & 0xffffu));
       out[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r[i] >> 16));
+    }
+  }
+};
+
+template <>
+struct Vec16<fp8e4m3> {
+  static constexpr int N = 16;
+  __device__ __forceinline__ static void to_f32(const u32x4& r, float* out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const f32x2 lo = __builtin_amdgcn_cvt_pk_f32_fp8((int)r[i], false);
+      const f32x2 hi = __builtin_amdgcn_cvt_pk_f32_fp8((int)r[i], true);
+      out[4 * i] = lo.x;
+      out[4 * i + 1] = lo.y;
+      out[4 * i + 2] = hi.x;
+      out[4 * i + 3] = hi.y;
     }
   }
 };

@@ -42,6 +42,8 @@
 //    are read exactly once per launch, so they use nontemporal (streaming)
 //    loads, which sustain markedly more HBM bandwidth for random row gathers
 //    on MI355X than default-policy loads.
+#include <type_traits>
+
 #include "msgl_common.h"
 
 namespace msgl {
@@ -88,6 +90,27 @@ struct QK<float> {
   }
 };
 
+// fp8 K elements -> the 16-bit MFMA B operand of the query's type. Every e4m3
+// value is exactly representable in bf16 and fp16, so the products on the
+// matrix core are those of the dequantised row up to its per-row scale.
+template <typename T>
+__device__ __forceinline__ u32x4 fp8x8_to(uint32_t w0, uint32_t w1);
+template <>
+__device__ __forceinline__ u32x4 fp8x8_to<bf16_t>(uint32_t w0, uint32_t w1) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+}
+template <>
+__device__ __forceinline__ u32x4 fp8x8_to<f16_t>(uint32_t w0, uint32_t w1) {
+  return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
+}
+
 // Split geometry of one request: chunks of the batch-wide length chunk_len
 // (the plan kernel's ceil(max_b L_b / max_splits), a multiple of 16 tokens),
 // at most max_splits of them, the last one taking the rest. Used identically
@@ -117,6 +140,7 @@ struct DecodeParams {
   const void* q;
   const void* k_pool;
   const void* v_pool;
+  const float* kv_scale;  // fp8 pools: [num_slots, Hkv, 2] (K, V) scales per slot and kv head
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
   const int32_t* seq_lens;
@@ -142,19 +166,22 @@ struct DecodeParams {
 constexpr int kLdsPerWave = 16 * 16 + 16 + 32;
 
 // One 16-token tile of K and V rows as loaded: both in row layout (LPR
-// consecutive lanes read one whole row, R rows per instruction).
-template <typename T, int D>
+// consecutive lanes read one whole row, R rows per instruction). KV is the
+// pool's storage type; an fp8 tile also carries the scales of the token this
+// lane's MFMA column holds.
+template <typename KV, int D>
 struct TileBuf {
-  static constexpr int VEC = QK<T>::VEC;
+  static constexpr int VEC = 16 / (int)sizeof(KV);
   static constexpr int NL = 16 / (64 / (D / VEC));
   u32x4 k[NL];
   u32x4 v[NL];
+  float ks, vs;
 };
 
 // Per-wave LDS K tile: 16 rows of D elements, row stride padded by 16 bytes so
 // row-wise writes and 16-row column reads are both free of bank conflicts.
-template <typename T, int D>
-constexpr int k_lds_stride() { return D * (int)sizeof(T) + 16; }
+template <typename KV, int D>
+constexpr int k_lds_stride() { return D * (int)sizeof(KV) + 16; }
 
 // Minimum wavefronts per SIMD the register allocator must allow (occupancy).
 #ifndef MSGL_DECODE_MIN_WAVES
@@ -164,29 +191,40 @@ constexpr int k_lds_stride() { return D * (int)sizeof(T) + 16; }
 #ifndef MSGL_DECODE_STAGES
 #define MSGL_DECODE_STAGES 2
 #endif
+#ifndef MSGL_DECODE_FP8_STAGES
+#define MSGL_DECODE_FP8_STAGES 2
+#endif
 
-template <typename T, int D, int G>
+// T: the query/output type; KV: the pool's storage type (T itself, or fp8e4m3
+// for a quantised pool with per-(slot, kv head) scales).
+template <typename T, typename KV, int D, int G>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(MSGL_DECODE_MIN_WAVES)))
 void paged_decode_kernel(DecodeParams p) {
-  constexpr int VEC = QK<T>::VEC;   // elements per 16-byte chunk
+  constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
+  constexpr int VEC = QK<T>::VEC;   // query elements per 16-byte chunk (MFMA operand)
   constexpr int ES = sizeof(T);
-  constexpr int KCHUNK = 4 * VEC;   // d covered by one K load across the 4 row groups
-  constexpr int NLK = D / KCHUNK;   // K loads per lane per 16-token tile
-  constexpr int LPR = D / VEC;      // lanes per V row
-  constexpr int R = 64 / LPR;       // V rows per wave load
-  constexpr int NLV = 16 / R;       // V loads per lane per tile
+  constexpr int VKV = 16 / (int)sizeof(KV);  // pool elements per 16-byte chunk
+  constexpr int EKV = sizeof(KV);
+  constexpr int KCHUNK = 4 * VEC;   // d covered by one MFMA step across the 4 row groups
+  constexpr int NLK = D / KCHUNK;   // MFMA steps per 16-token tile
+  constexpr int LPR = D / VKV;      // lanes per K/V row
+  constexpr int R = 64 / LPR;       // K/V rows per wave load
+  constexpr int NLV = 16 / R;       // K/V loads per lane per tile
   constexpr int NR = G < 4 ? G : 4; // MFMA accumulator rows holding query heads
-  constexpr int NST = (sizeof(T) == 4 || D > 128 || G > 4) ? 2 : MSGL_DECODE_STAGES;  // register budget
+  // register budget; fp8 tiles are half the bytes, so they keep more in flight
+  constexpr int NST = Q8 ? (G <= 2 && D <= 128 ? MSGL_DECODE_FP8_STAGES : 2)
+                         : ((sizeof(T) == 4 || D > 128 || G > 4) ? 2 : MSGL_DECODE_STAGES);
   static_assert(NST >= 2 && (NST - 1) * 16 <= kSlotPad, "pipeline depth");
   static_assert(D % KCHUNK == 0 && 64 % LPR == 0 && 16 % R == 0, "unsupported head_dim");
   static_assert(G >= 1 && G <= 16, "unsupported group size");
+  static_assert(!Q8 || (sizeof(T) == 2 && G <= 8), "fp8 pools take 16-bit queries and groups up to 8");
 
   extern __shared__ float lds_all[];
   int* slots_lds = reinterpret_cast<int*>(lds_all);  // [kSeg + kSlotPad]
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int nwaves = blockDim.x >> 6;
-  constexpr int KRS = k_lds_stride<T, D>();
+  constexpr int KRS = k_lds_stride<KV, D>();
   float* lds = lds_all + kSeg + kSlotPad + wave * (kLdsPerWave + 16 * KRS / 4);
   float* P_lds = lds;              // [16][16]
   float* A_lds = lds + 256;        // [16]
@@ -221,7 +259,7 @@ void paged_decode_kernel(DecodeParams p) {
   const int vc = lane % LPR;  // V: 16-byte chunk within the row
   const int vr = lane / LPR;  // V: token sub-row
 
-  const int64_t row_stride = (int64_t)p.hkv * D * ES;  // bytes per slot
+  const int64_t row_stride = (int64_t)p.hkv * D * EKV;  // bytes per slot
 
   {
     const int kvh = kgrp * nwaves + wave;
@@ -244,19 +282,20 @@ void paged_decode_kernel(DecodeParams p) {
       m_run[i] = -INFINITY;
       l_run[i] = 0.f;
     }
-    float acc[G][VEC];
+    float acc[G][VKV];
 #pragma unroll
     for (int g = 0; g < G; ++g)
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) acc[g][e] = 0.f;
+      for (int e = 0; e < VKV; ++e) acc[g][e] = 0.f;
 
-    const uint8_t* kbase_p = reinterpret_cast<const uint8_t*>(p.k_pool) + (int64_t)kvh_c * D * ES + vc * VEC * ES;
-    const uint8_t* vbase_p = reinterpret_cast<const uint8_t*>(p.v_pool) + (int64_t)kvh_c * D * ES + vc * VEC * ES;
+    const uint8_t* kbase_p = reinterpret_cast<const uint8_t*>(p.k_pool) + (int64_t)kvh_c * D * EKV + vc * 16;
+    const uint8_t* vbase_p = reinterpret_cast<const uint8_t*>(p.v_pool) + (int64_t)kvh_c * D * EKV + vc * 16;
 
-    // Fused KV store: the chunk holding position L-1 (the new token) writes its
-    // rows to the pool and reads them from k_new/v_new instead -- no other
-    // unit reads that slot, so the write needs no ordering inside the launch.
-    const bool fused = p.k_new != nullptr;
+    // Fused KV store (unquantised pools): the chunk holding position L-1 (the
+    // new token) writes its rows to the pool and reads them from k_new/v_new
+    // instead -- no other unit reads that slot, so the write needs no ordering
+    // inside the launch.
+    const bool fused = !Q8 && p.k_new != nullptr;
     const int new_pos = fused && t1 == L ? L - 1 : 0x7fffffff;  // absolute position, or never
     const int64_t new_off = ((int64_t)b * p.hkv + kvh_c) * D * ES + vc * VEC * ES;
     const uint8_t* knew_p = fused ? reinterpret_cast<const uint8_t*>(p.k_new) + new_off : nullptr;
@@ -287,7 +326,7 @@ void paged_decode_kernel(DecodeParams p) {
       // valid slot, one row per tile, already fetched): every path through the
       // loop keeps the same loads in flight, so the compiler waits for exactly
       // one tile instead of draining the pipeline at each branch.
-      auto issue = [&](TileBuf<T, D>& buf, int tile) {
+      auto issue = [&](TileBuf<KV, D>& buf, int tile) {
         const int base = tile * 16;
 #pragma unroll
         for (int i = 0; i < NLV; ++i) {
@@ -297,9 +336,14 @@ void paged_decode_kernel(DecodeParams p) {
           buf.k[i] = ld16_stream(is_new ? knew_p : kbase_p + off);
           buf.v[i] = ld16_stream(is_new ? vnew_p : vbase_p + off);
         }
+        if (Q8) {  // the K and V scales of the token in this lane's MFMA column: one 8-byte load
+          const float2 sc = reinterpret_cast<const float2*>(p.kv_scale)[(int64_t)slots_lds[base + r] * p.hkv + kvh_c];
+          buf.ks = sc.x;
+          buf.vs = sc.y;
+        }
       };
 
-      auto compute = [&](const TileBuf<T, D>& buf, int tile) {
+      auto compute = [&](const TileBuf<KV, D>& buf, int tile) {
         // K rows -> LDS -> MFMA B layout (lane: token r, d chunk j*KCHUNK + g4*VEC)
         wave_lds_sync();
 #pragma unroll
@@ -308,14 +352,22 @@ void paged_decode_kernel(DecodeParams p) {
         // S = Q K^T on the matrix core
         f32x4 s = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int j = 0; j < NLK; ++j)
-          s = QK<T>::step(qa[j], *reinterpret_cast<const u32x4*>(K_lds + r * KRS + (j * KCHUNK + g4 * VEC) * ES), s);
-        // online softmax (exp2 domain)
+        for (int j = 0; j < NLK; ++j) {
+          if constexpr (Q8) {
+            const uint2 k8 = *reinterpret_cast<const uint2*>(K_lds + r * KRS + (j * KCHUNK + g4 * VEC));
+            s = QK<T>::step(qa[j], fp8x8_to<T>(k8.x, k8.y), s);
+          } else {
+            s = QK<T>::step(qa[j], *reinterpret_cast<const u32x4*>(K_lds + r * KRS + (j * KCHUNK + g4 * VEC) * ES),
+                            s);
+          }
+        }
+        // online softmax (exp2 domain); a quantised row's scale multiplies its scores
+        const float sc = Q8 ? p.scale_log2 * buf.ks : p.scale_log2;
         const bool valid = tile * 16 + r < seg_len;
         float pr[4] = {0.f, 0.f, 0.f, 0.f}, al[4] = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
-          const float x = valid ? s[i] * p.scale_log2 : -INFINITY;
+          const float x = valid ? s[i] * sc : -INFINITY;
           const float mt = row16_max(x);
           const float m_new = fmaxf(m_run[i], mt);
           al[i] = __builtin_amdgcn_exp2f(m_run[i] - m_new);
@@ -324,7 +376,9 @@ void paged_decode_kernel(DecodeParams p) {
           m_run[i] = m_new;
         }
         wave_lds_sync();  // previous tile's LDS reads are done
-        *reinterpret_cast<f32x4*>(P_lds + r * 16 + 4 * g4) = f32x4{pr[0], pr[1], pr[2], pr[3]};
+        // P V weights; a quantised V row's scale is folded into its weight (l keeps the plain weights)
+        const float vsc = Q8 ? buf.vs : 1.f;
+        *reinterpret_cast<f32x4*>(P_lds + r * 16 + 4 * g4) = f32x4{pr[0] * vsc, pr[1] * vsc, pr[2] * vsc, pr[3] * vsc};
         if (r == 0) *reinterpret_cast<f32x4*>(A_lds + 4 * g4) = f32x4{al[0], al[1], al[2], al[3]};
         wave_lds_sync();
         // O = alpha * O + P V on the VALU
@@ -334,24 +388,24 @@ void paged_decode_kernel(DecodeParams p) {
 #pragma unroll
         for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) acc[g][e] *= alpha[g];
+          for (int e = 0; e < VKV; ++e) acc[g][e] *= alpha[g];
 #pragma unroll
         for (int i = 0; i < NLV; ++i) {
           const int tl = vr + R * i;
-          float vf[VEC];
-          Vec16<T>::to_f32(buf.v[i], vf);
+          float vf[VKV];
+          Vec16<KV>::to_f32(buf.v[i], vf);
           float pv[G];
 #pragma unroll
           for (int g = 0; g < G; ++g) pv[g] = P_lds[tl * 16 + g];
 #pragma unroll
           for (int g = 0; g < G; ++g)
 #pragma unroll
-            for (int e = 0; e < VEC; ++e) acc[g][e] = fmaf(pv[g], vf[e], acc[g][e]);
+            for (int e = 0; e < VKV; ++e) acc[g][e] = fmaf(pv[g], vf[e], acc[g][e]);
         }
       };
 
       // NST-stage register pipeline: tiles t+1 .. t+NST-1 are in flight while t computes
-      TileBuf<T, D> buf[NST];
+      TileBuf<KV, D> buf[NST];
 #pragma unroll
       for (int i = 0; i < NST - 1; ++i) issue(buf[i], i);  // tiles past ntile are padding
       for (int tile = 0; tile < ntile; tile += NST) {
@@ -374,7 +428,7 @@ void paged_decode_kernel(DecodeParams p) {
 #pragma unroll
       for (int g = 0; g < G; ++g)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+        for (int e = 0; e < VKV; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
     wave_lds_sync();
     if (r == 0) {
 #pragma unroll
@@ -384,19 +438,22 @@ void paged_decode_kernel(DecodeParams p) {
       }
     }
     wave_lds_sync();
-    const int d0 = vc * VEC;
+    const int d0 = vc * VKV;
     if (n == 1) {
       if (lane < LPR) {
         T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D + d0;
 #pragma unroll
         for (int g = 0; g < G; ++g) {
           const float inv = 1.f / ML_lds[g * 2 + 1];
-          T tmp[VEC];
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) tmp[e] = from_f32<T>(acc[g][e] * inv);
-          u32x4 packed;
-          __builtin_memcpy(&packed, tmp, 16);
-          st16(o + g * D, packed);
+          for (int c = 0; c < VKV; c += VEC) {
+            T tmp[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) tmp[e] = from_f32<T>(acc[g][c + e] * inv);
+            u32x4 packed;
+            __builtin_memcpy(&packed, tmp, 16);
+            st16(o + g * D + c, packed);
+          }
         }
       }
       return;
@@ -409,7 +466,7 @@ void paged_decode_kernel(DecodeParams p) {
       for (int g = 0; g < G; ++g) {
         float* po = p.part_o + (base + g) * D + d0;
 #pragma unroll
-        for (int e = 0; e < VEC; e += 4)
+        for (int e = 0; e < VKV; e += 4)
           *reinterpret_cast<f32x4*>(po + e) = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
       }
     }
@@ -566,17 +623,17 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeP
   }
 }
 
-template <typename T, int D, int G>
+template <typename T, typename KV, int D, int G>
 static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
   const int nwaves = p.hkv < MSGL_DECODE_WAVES_PER_WG ? p.hkv : MSGL_DECODE_WAVES_PER_WG;
-  const size_t lds = ((size_t)kSeg + kSlotPad + (size_t)nwaves * (kLdsPerWave + 16 * k_lds_stride<T, D>() / 4)) *
+  const size_t lds = ((size_t)kSeg + kSlotPad + (size_t)nwaves * (kLdsPerWave + 16 * k_lds_stride<KV, D>() / 4)) *
                      sizeof(float);
   if (!p.planned) {
     hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
     MSGL_CHECK_LAUNCH("msgl_paged_decode (plan)");
   }
-  hipLaunchKernelGGL((paged_decode_kernel<T, D, G>), dim3(batch * p.max_splits * p.ngrp), dim3(64 * nwaves), lds,
-                     stream, p);
+  hipLaunchKernelGGL((paged_decode_kernel<T, KV, D, G>), dim3(batch * p.max_splits * p.ngrp), dim3(64 * nwaves),
+                     lds, stream, p);
   MSGL_CHECK_LAUNCH("msgl_paged_decode");
   if (p.max_splits > 1) {
     const int units = batch * p.hkv;
@@ -586,26 +643,29 @@ static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
   return MSGL_OK;
 }
 
-template <typename T, int D>
+template <typename T, typename KV, int D>
 static int dispatch_group(const DecodeParams& p, int batch, int group, hipStream_t stream) {
+  constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
   switch (group) {
-    case 1: return launch_decode<T, D, 1>(p, batch, stream);
-    case 2: return launch_decode<T, D, 2>(p, batch, stream);
-    case 4: return launch_decode<T, D, 4>(p, batch, stream);
-    case 8: return launch_decode<T, D, 8>(p, batch, stream);
-    case 16: return launch_decode<T, D, 16>(p, batch, stream);
+    case 1: return launch_decode<T, KV, D, 1>(p, batch, stream);
+    case 2: return launch_decode<T, KV, D, 2>(p, batch, stream);
+    case 4: return launch_decode<T, KV, D, 4>(p, batch, stream);
+    case 8: return launch_decode<T, KV, D, 8>(p, batch, stream);
+    case 16:
+      if constexpr (!Q8) return launch_decode<T, KV, D, 16>(p, batch, stream);
+      [[fallthrough]];
     default:
-      set_error("msgl_paged_decode: Hq/Hkv = %d not built (1, 2, 4, 8, 16)", group);
+      set_error("msgl_paged_decode: Hq/Hkv = %d not built (1, 2, 4, 8%s)", group, Q8 ? " for fp8 pools" : ", 16");
       return MSGL_ERR_UNSUPPORTED;
   }
 }
 
-template <typename T>
+template <typename T, typename KV = T>
 static int dispatch_dim(const DecodeParams& p, int batch, int head_dim, int group, hipStream_t stream) {
   switch (head_dim) {
-    case 64: return dispatch_group<T, 64>(p, batch, group, stream);
-    case 128: return dispatch_group<T, 128>(p, batch, group, stream);
-    case 256: return dispatch_group<T, 256>(p, batch, group, stream);
+    case 64: return dispatch_group<T, KV, 64>(p, batch, group, stream);
+    case 128: return dispatch_group<T, KV, 128>(p, batch, group, stream);
+    case 256: return dispatch_group<T, KV, 256>(p, batch, group, stream);
     default:
       set_error("msgl_paged_decode: head_dim %d not built (64, 128, 256)", head_dim);
       return MSGL_ERR_UNSUPPORTED;
@@ -668,8 +728,9 @@ extern "C" int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_q
 enum DecodeMode { kPlanAndRun, kRunPlanned };
 
 static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, const void* k_new, const void* v_new,
-                             const int32_t* out_loc, const void* k_pool, const void* v_pool,
-                             const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                             const int32_t* out_loc, const void* k_pool, const void* v_pool, const float* kv_scale,
+                             const int32_t* kv_indptr, const int32_t* kv_indices,
+                             const int32_t* seq_lens,
                              int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                              int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
                              void* out, void* workspace, int64_t workspace_bytes, void* stream);
@@ -679,7 +740,8 @@ extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* 
                                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                  int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                                  void* workspace, int64_t workspace_bytes, void* stream) {
-  return paged_decode_impl("msgl_paged_decode", kPlanAndRun, q, nullptr, nullptr, nullptr, k_pool, v_pool, kv_indptr,
+  return paged_decode_impl("msgl_paged_decode", kPlanAndRun, q, nullptr, nullptr, nullptr, k_pool, v_pool, nullptr,
+                           kv_indptr,
                            kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size, num_slots,
                            dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
 }
@@ -726,7 +788,7 @@ extern "C" int msgl_paged_decode_planned(const void* q, const void* k_pool, cons
                                          int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
                                          int64_t workspace_bytes, void* stream) {
   return paged_decode_impl("msgl_paged_decode_planned", kRunPlanned, q, nullptr, nullptr, nullptr, k_pool, v_pool,
-                           kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
+                           nullptr, kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
                            num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
 }
 
@@ -743,7 +805,7 @@ extern "C" int msgl_paged_decode_store(const void* q, const void* k_new, const v
   MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
                  "msgl_paged_decode_store: k_new and v_new must be 16-byte aligned");
   return paged_decode_impl("msgl_paged_decode_store", kPlanAndRun, q, k_new, v_new, out_loc, k_pool, v_pool,
-                           kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
+                           nullptr, kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
                            num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
 }
 
@@ -760,13 +822,44 @@ extern "C" int msgl_paged_decode_store_planned(const void* q, const void* k_new,
   MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
                  "msgl_paged_decode_store_planned: k_new and v_new must be 16-byte aligned");
   return paged_decode_impl("msgl_paged_decode_store_planned", kRunPlanned, q, k_new, v_new, out_loc, k_pool, v_pool,
-                           kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
+                           nullptr, kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim, page_size,
                            num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
 }
 
+extern "C" int msgl_paged_decode_fp8(const void* q, const void* k_pool, const void* v_pool, const float* kv_scale,
+                                     const int32_t* kv_indptr, const int32_t* kv_indices,
+                                     const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                     int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                                     int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                                     int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(kv_scale != nullptr, "msgl_paged_decode_fp8: null kv_scale");
+  return paged_decode_impl("msgl_paged_decode_fp8", kPlanAndRun, q, nullptr, nullptr, nullptr, k_pool, v_pool, kv_scale,
+                           kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim,
+                           page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int msgl_paged_decode_fp8_planned(const void* q, const void* k_pool, const void* v_pool,
+                                             const float* kv_scale, const int32_t* kv_indptr,
+                                             const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                                             int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                             int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                                             int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
+                                             void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(kv_scale != nullptr, "msgl_paged_decode_fp8_planned: null kv_scale");
+  return paged_decode_impl("msgl_paged_decode_fp8_planned", kRunPlanned, q, nullptr, nullptr, nullptr, k_pool, v_pool,
+                           kv_scale, kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads,
+                           head_dim, page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes,
+                           stream);
+}
+
 static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, const void* k_new, const void* v_new,
-                             const int32_t* out_loc, const void* k_pool, const void* v_pool,
-                             const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                             const int32_t* out_loc, const void* k_pool, const void* v_pool, const float* kv_scale,
+                             const int32_t* kv_indptr, const int32_t* kv_indices,
+                             const int32_t* seq_lens,
                              int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                              int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
                              void* out, void* workspace, int64_t workspace_bytes, void* stream) {
@@ -784,6 +877,7 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
   MSGL_CHECK_ARG(q && k_pool && v_pool && kv_indptr && kv_indices && out, "%s: null pointer", fn);
   MSGL_CHECK_ARG(((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) % 16 == 0,
                  "%s: q, pools and out must be 16-byte aligned", fn);
+  MSGL_CHECK_ARG((uintptr_t)kv_scale % 8 == 0, "%s: kv_scale must be 8-byte aligned", fn);
   if (dtype_size(dtype) == 0) {
     set_error("%s: unknown dtype %d", fn, dtype);
     return MSGL_ERR_UNSUPPORTED;
@@ -801,6 +895,7 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
   p.q = q;
   p.k_pool = k_pool;
   p.v_pool = v_pool;
+  p.kv_scale = kv_scale;
   p.kv_indptr = kv_indptr;
   p.kv_indices = kv_indices;
   p.seq_lens = seq_lens;
@@ -827,6 +922,14 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
   p.scale_log2 = scale * kLog2e;
   const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
+  if (kv_scale != nullptr) {  // fp8 e4m3 pools with per-(slot, kv head) scales
+    switch (dtype) {
+      case MSGL_BF16: return dispatch_dim<bf16_t, fp8e4m3>(p, batch, head_dim, group, s);
+      case MSGL_F16: return dispatch_dim<f16_t, fp8e4m3>(p, batch, head_dim, group, s);
+    }
+    set_error("%s: fp8 pools take bf16 or fp16 queries (dtype %d)", fn, dtype);
+    return MSGL_ERR_UNSUPPORTED;
+  }
   switch (dtype) {
     case MSGL_F32: return dispatch_dim<float>(p, batch, head_dim, group, s);
     case MSGL_BF16: return dispatch_dim<bf16_t>(p, batch, head_dim, group, s);

@@ -55,6 +55,37 @@ def store_kv(
     _lib.check(status, "msgl_store_kv")
 
 
+def store_kv_fp8(
+    k: torch.Tensor, v: torch.Tensor, out_loc: torch.Tensor, k_pool: torch.Tensor, v_pool: torch.Tensor,
+    kv_scale: torch.Tensor,
+) -> None:
+    """kvcache/pool.py:47-50 into an fp8 pool: per (token, kv head) row, codes
+    e4m3(x * 448 / amax) in k_pool/v_pool (``torch.float8_e4m3fn`` [N, Hkv, D])
+    and scale amax / 448 in kv_scale (float32 [N, Hkv, 2]: K scale, V scale), in place."""
+    if k.dim() != 3 or k.shape != v.shape:
+        raise ValueError(f"k/v must both be [T, Hkv, D] (got {tuple(k.shape)}, {tuple(v.shape)})")
+    if k_pool.dtype != torch.float8_e4m3fn or v_pool.dtype != torch.float8_e4m3fn:
+        raise ValueError("pools must be torch.float8_e4m3fn")
+    if k_pool.dim() != 3 or k_pool.shape != v_pool.shape or k_pool.shape[1:] != k.shape[1:]:
+        raise ValueError(f"pools must be [N, Hkv, D] matching k (got {tuple(k_pool.shape)})")
+    n, hkv = k_pool.shape[:2]
+    if kv_scale.dtype != torch.float32 or kv_scale.shape != (n, hkv, 2):
+        raise ValueError("kv_scale must be float32 [N, Hkv, 2]")
+    if out_loc.shape != (k.shape[0],):
+        raise ValueError("out_loc must be [T]")
+    if k.dtype != v.dtype:
+        raise ValueError("k and v must share one dtype")
+    dev = k_pool.device
+    for name, t in (("k", k), ("v", v), ("k_pool", k_pool), ("v_pool", v_pool), ("kv_scale", kv_scale)):
+        _check_device(name, t, dev)
+    _check_index("out_loc", out_loc, dev)
+    status = _lib.load().msgl_store_kv_fp8(
+        _lib.ptr(k), _lib.ptr(v), _lib.ptr(out_loc), _lib.ptr(k_pool), _lib.ptr(v_pool), _lib.ptr(kv_scale),
+        k.shape[0], k.shape[1], k.shape[2], n, _lib.dtype_code(k.dtype), _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_store_kv_fp8")
+
+
 def default_splits(batch: int, num_kv_heads: int, max_seq_len: int = 0) -> int:
     return int(_lib.load().msgl_paged_decode_default_splits(batch, num_kv_heads, max_seq_len))
 
@@ -140,8 +171,13 @@ def paged_decode_attention(
     workspace: Optional[torch.Tensor] = None,
     new_kv: Optional[tuple] = None,
     planned: bool = False,
+    kv_scale: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Paged decode attention; counterpart of attention/metal.py:112-131.
+
+    fp8 pools (``torch.float8_e4m3fn``, written by ``store_kv_fp8``) take
+    ``kv_scale`` (float32 [N, Hkv, 2]: K scale, V scale); q is bf16/fp16 and the
+    result is the decode over the dequantised pool (no fused store).
 
     q [B, Hq, D]; pools [N, Hkv, D]; kv_indptr [B+1] int32; kv_indices int32
     (token slots, or page ids when page_size > 1 with seq_lens [B] given).
@@ -159,7 +195,16 @@ def paged_decode_attention(
     n_slots, hkv, dk = k_pool.shape
     if dk != d or hq % hkv != 0:
         raise ValueError(f"head_dim mismatch or Hq ({hq}) not a multiple of Hkv ({hkv})")
-    if len({q.dtype, k_pool.dtype, v_pool.dtype}) != 1:
+    fp8 = k_pool.dtype == torch.float8_e4m3fn
+    if fp8:
+        if v_pool.dtype != k_pool.dtype or kv_scale is None or new_kv is not None:
+            raise ValueError("fp8 pools need both pools fp8, kv_scale and no new_kv")
+        if q.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("fp8 pools take bf16 or fp16 queries")
+        if kv_scale.dtype != torch.float32 or kv_scale.shape != (n_slots, hkv, 2):
+            raise ValueError("kv_scale must be float32 [N, Hkv, 2]")
+        _check_device("kv_scale", kv_scale, q.device)
+    elif len({q.dtype, k_pool.dtype, v_pool.dtype}) != 1:
         raise ValueError("q and pools must share one dtype")
     if page_size > 1 and seq_lens is None:
         raise ValueError("page_size > 1 needs seq_lens")
@@ -192,7 +237,11 @@ def paged_decode_attention(
         b, hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
         max_splits, _lib.ptr(out), _lib.ptr(workspace), ws_bytes, _lib.current_stream(dev),
     )
-    if new_kv is None:
+    if fp8:
+        fn = lib.msgl_paged_decode_fp8_planned if planned else lib.msgl_paged_decode_fp8
+        status = fn(_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool), _lib.ptr(kv_scale), *common)
+        _lib.check(status, "msgl_paged_decode_fp8")
+    elif new_kv is None:
         fn = lib.msgl_paged_decode_planned if planned else lib.msgl_paged_decode
         status = fn(_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool), *common)
         _lib.check(status, "msgl_paged_decode")

@@ -15,14 +15,16 @@ It restates, in numpy, the reference's algorithm for the attention path
 - attention (fp64 accumulation): ``attention/naive.py:50-60`` (decode),
   ``attention/base.py:85-105`` (prefill, bottom-right causal);
 - rotary embedding and the rotate-then-store order: ``layers.py:19-74, 107-109``
-  (``rope.py``).
+  (``rope.py``);
+- an fp8 (e4m3) KV cache with one scale per token and kv head, the extension
+  docs/09-exercises.md:81-82 describes (``kv_quant.py``).
 
 Every function is pinned by a check in ``tests/test_oracle.py`` that does not
 retype its formula: closed forms (one key gives that key's value row, equal
 keys give the mean of the values), brute-force Python loops on tiny inputs,
 an independent library routine (``torch.nn.functional.scaled_dot_product_attention``
 on the CPU), the rotary embedding of ``transformers`` (``apply_rotary_pos_emb`` and its
-llama3 / linear frequency initialisers), the reference test's fixture construction
+llama3 / linear frequency initialisers), torch's ``float8_e4m3fn`` casts, the reference test's fixture construction
 (``tests/test_attention.py:19-39``) and the page-layout assertion of
 ``tests/test_cache_manager.py:66-75``, plus mutation tests that plant a
 mistake in a copy of the oracle and show the checks catch it.
@@ -51,4 +53,12 @@ from .rope import (  # noqa: F401
     rope_periods,
     rope_position_scale,
     rope_store_kv,
+)
+from .kv_quant import (  # noqa: F401
+    E4M3_MAX,
+    dequantize_fp8,
+    e4m3_decode,
+    e4m3_encode,
+    quantize_fp8,
+    store_kv_fp8,
 )

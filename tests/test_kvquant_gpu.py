@@ -1,0 +1,160 @@
+"""fp8 KV cache on the GPU vs the oracle: the quantising store bit for bit
+(codes and scales), and paged decode over fp8 pools against the float64 decode
+of the dequantised pool (attention/naive.py:50-60 semantics), over the
+reference test's shape grid, split settings, page ids and the headline batch."""
+
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from gpu_util import DTYPES, assert_close, i32, randn, to_np64
+from minisgl_hip import ops, workloads
+
+pytestmark = pytest.mark.gpu
+
+FP8 = torch.float8_e4m3fn
+
+
+def _codes(t):
+    return t.view(torch.uint8).cpu().numpy()
+
+
+def _fp8_pools(n, hkv, d, seed, device, src_dtype=torch.bfloat16, spread=True):
+    """Quantise random rows into every slot with the HIP store; returns (kp, vp, kv_scale, k_src, v_src)."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    k = torch.randn((n, hkv, d), generator=g, device=device, dtype=torch.float32)
+    v = torch.randn((n, hkv, d), generator=g, device=device, dtype=torch.float32)
+    if spread:  # rows of very different magnitudes, so the per-row scales matter
+        k *= torch.exp(torch.randn((n, hkv, 1), generator=g, device=device) * 2)
+        v *= torch.exp(torch.randn((n, hkv, 1), generator=g, device=device) * 2)
+    k, v = k.to(src_dtype), v.to(src_dtype)
+    kp = torch.empty((n, hkv, d), dtype=FP8, device=device)
+    vp = torch.empty_like(kp)
+    sc = torch.empty((n, hkv, 2), dtype=torch.float32, device=device)
+    ops.store_kv_fp8(k, v, torch.arange(n, dtype=torch.int32, device=device), kp, vp, sc)
+    return kp, vp, sc, k, v
+
+
+def _deq(codes, sc, which):
+    """Dequantised pool from the codes and column `which` (0 = K, 1 = V) of kv_scale."""
+    return oracle.dequantize_fp8(_codes(codes), sc[..., which].cpu().numpy())
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16", "f32"])
+@pytest.mark.parametrize("hkv,d", [(8, 128), (2, 64), (4, 256)])
+def test_store_kv_fp8_bit_exact(cuda_device, dt, hkv, d):
+    dtype = DTYPES[dt]
+    t, n = 300, 4096
+    g = torch.Generator().manual_seed(5)
+    spread = 1.0 if dtype == torch.float16 else 3.0  # row magnitudes over many binades, finite in fp16
+    k = (torch.randn((t, hkv, d), generator=g) * torch.exp(torch.randn((t, hkv, 1), generator=g) * spread)).to(dtype)
+    v = (torch.randn((t, hkv, d), generator=g) * torch.exp(torch.randn((t, hkv, 1), generator=g) * spread)).to(dtype)
+    k[7, 0] = 0.0  # zero rows: codes 0, scale 0
+    v[9] = -0.0
+    k, v = k.to(cuda_device), v.to(cuda_device)
+    kp0 = torch.randint(0, 126, (n, hkv, d), dtype=torch.uint8, device=cuda_device)
+    kp, vp = kp0.clone().view(FP8), kp0.clone().view(FP8)
+    sc = torch.full((n, hkv, 2), 3.0, device=cuda_device)
+    loc = np.random.default_rng(6).permutation(n)[:t].astype(np.int32)
+    print(f"case store_kv_fp8 {dt} hkv={hkv} d={d}", flush=True)
+    ops.store_kv_fp8(k, v, i32(loc, cuda_device), kp, vp, sc)
+    torch.cuda.synchronize()
+    ks, vs = sc[..., 0], sc[..., 1]
+    kc, ksc = oracle.quantize_fp8(to_np64(k).astype(np.float32))
+    vc, vsc = oracle.quantize_fp8(to_np64(v).astype(np.float32))
+    np.testing.assert_array_equal(_codes(kp)[loc], kc)
+    np.testing.assert_array_equal(_codes(vp)[loc], vc)
+    np.testing.assert_array_equal(ks.cpu().numpy()[loc], ksc)
+    np.testing.assert_array_equal(vs.cpu().numpy()[loc], vsc)
+    rest = np.setdiff1d(np.arange(n), loc)
+    np.testing.assert_array_equal(_codes(kp)[rest], kp0.cpu().numpy()[rest])
+    assert (ks.cpu().numpy()[rest] == 3.0).all()
+
+
+def test_store_kv_fp8_skips_slots_outside_pool(cuda_device):
+    k = randn((3, 2, 64), 1, torch.bfloat16).to(cuda_device)
+    kp = torch.zeros((8, 2, 64), dtype=torch.uint8, device=cuda_device).view(FP8)
+    vp = torch.zeros_like(kp)
+    sc = torch.zeros((8, 2, 2), device=cuda_device)
+    ops.store_kv_fp8(k, k, i32([-1, 8, 5], cuda_device), kp, vp, sc)
+    torch.cuda.synchronize()
+    ks = sc[..., 0]
+    written = np.zeros(8, bool)
+    written[5] = True
+    assert not _codes(kp)[~written].any() and not ks.cpu().numpy()[~written].any()
+    assert _codes(kp)[5].any() and (ks.cpu().numpy()[5] > 0).all()
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256), (64, 8, 128)])
+@pytest.mark.parametrize("splits", [1, None, 8])
+def test_fp8_decode_reference_grid(cuda_device, dt, hq, hkv, d, splits):
+    """tests/test_attention.py:19-39's grid (B=7, lens [1,2,17,31,32,33,700], N=4096) over fp8 pools."""
+    dtype = DTYPES[dt]
+    c = workloads.reference_test_case()
+    kp, vp, sc, _, _ = _fp8_pools(4096, hkv, d, 100, cuda_device)
+    q = randn((7, hq, d), 102, dtype).to(cuda_device)
+    print(f"case fp8 grid hq={hq} hkv={hkv} d={d} {dt} splits={splits}", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device),
+                                     d**-0.5, max_splits=splits, kv_scale=sc)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(to_np64(q), _deq(kp, sc, 0), _deq(vp, sc, 1), c.kv_indptr, c.kv_indices, d**-0.5)
+    assert_close(out, ref, dtype, f"fp8 grid {hq}/{hkv}/{d} {dt} splits={splits}")
+
+
+@pytest.mark.parametrize("splits", [1, 4, 64])
+def test_fp8_decode_edge_lengths_and_pages(cuda_device, splits):
+    lens = [1, 15, 16, 17, 63, 64, 65, 127, 128, 129, 1000, 4097]
+    for page in (1, 16):
+        c = workloads.decode_case_from_lens(lens, num_slots=16384, page_size=page, seed=7)
+        kp, vp, sc, _, _ = _fp8_pools(16384, 8, 128, 200, cuda_device)
+        q = randn((len(lens), 16, 128), 202, torch.bfloat16).to(cuda_device)
+        print(f"case fp8 edge page={page} splits={splits}", flush=True)
+        kwargs = dict(seq_lens=i32(c.lens, cuda_device), page_size=page) if page > 1 else {}
+        indptr = c.page_indptr if page > 1 else c.kv_indptr
+        indices = c.page_ids if page > 1 else c.kv_indices
+        out = ops.paged_decode_attention(q, kp, vp, i32(indptr, cuda_device), i32(indices, cuda_device),
+                                         128**-0.5, max_splits=splits, kv_scale=sc, **kwargs)
+        torch.cuda.synchronize()
+        ref = oracle.paged_decode(to_np64(q), _deq(kp, sc, 0), _deq(vp, sc, 1), c.kv_indptr, c.kv_indices, 128**-0.5)
+        assert_close(out, ref, torch.bfloat16, f"fp8 edge page={page} splits={splits}")
+
+
+def test_fp8_planned_matches_unplanned(cuda_device):
+    c = workloads.decode_case(64, 10, 3000, 131072, 1, seed=3)
+    kp, vp, sc, _, _ = _fp8_pools(131072, 8, 128, 300, cuda_device)
+    q = randn((64, 32, 128), 301, torch.bfloat16).to(cuda_device)
+    ip, ix = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    splits = ops.default_splits(64, 8, int(c.lens.max()))
+    ws = ops.decode_workspace(64, 32, 8, 128, splits, cuda_device)
+    a = ops.paged_decode_attention(q, kp, vp, ip, ix, 128**-0.5, max_splits=splits, kv_scale=sc)
+    ops.paged_decode_plan(ip, None, 64, 32, 8, 128, splits, ws)
+    b = ops.paged_decode_attention(q, kp, vp, ip, ix, 128**-0.5, max_splits=splits, kv_scale=sc,
+                                   workspace=ws, planned=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, b)
+
+
+def test_fp8_decode_headline_batch(cuda_device):
+    """The headline decode shape (batch 128, L ~ U[200, 2048], 262144-slot pool) over an fp8 pool:
+    sampled requests vs the oracle, and the quantisation error against the unquantised decode."""
+    c = workloads.decode_case(128, 200, 2048, 262144, 1, seed=0)
+    kp, vp, sc, k_src, v_src = _fp8_pools(262144, 8, 128, 400, cuda_device, spread=False)
+    q = randn((128, 16, 128), 401, torch.bfloat16).to(cuda_device)
+    ip, ix = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    print("case fp8 headline", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, ip, ix, 128**-0.5, kv_scale=sc)
+    exact = ops.paged_decode_attention(q, k_src, v_src, ip, ix, 128**-0.5)
+    torch.cuda.synchronize()
+    for b in (0, 17, 64, 127):
+        s, e = int(c.kv_indptr[b]), int(c.kv_indptr[b + 1])
+        slots = torch.from_numpy(c.kv_indices[s:e].astype(np.int64)).to(cuda_device)
+        kb = oracle.dequantize_fp8(_codes(kp[slots]), sc[slots][..., 0].cpu().numpy())
+        vb = oracle.dequantize_fp8(_codes(vp[slots]), sc[slots][..., 1].cpu().numpy())
+        ref = oracle.paged_decode(to_np64(q[b:b + 1]), kb, vb, np.array([0, e - s]), np.arange(e - s), 128**-0.5)
+        assert_close(out[b:b + 1], ref, torch.bfloat16, f"fp8 headline request {b}")
+    # e4m3 keeps 3 mantissa bits: outputs stay within a few percent of the unquantised decode
+    rel = ((out.float() - exact.float()).norm() / exact.float().norm()).item()
+    print(f"fp8 vs bf16 decode relative error {rel:.4f}", flush=True)
+    assert rel < 0.05
