@@ -361,6 +361,30 @@ def _timed(args, run, timed_call=None):
     return elapsed, ev_s
 
 
+def _b2b_step_time(args, fn, n):
+    """Median GPU time of one step = n calls fn(0..n-1) back to back. A spin
+    kernel holds the stream while the host enqueues the step, so the events
+    bracket GPU work only (the Python wrappers can need longer per call than a
+    short launch runs)."""
+    import torch
+
+    for _ in range(args.warmup):
+        for i in range(n):
+            fn(i)
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(args.steps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        torch.cuda._sleep(250_000 * n)  # ~120 us of spin per call: longer than the host needs to enqueue it
+        a.record()
+        for i in range(n):
+            fn(i)
+        b.record()
+        torch.cuda.synchronize()
+        times.append(a.elapsed_time(b) / 1e3)
+    return float(np.median(times))
+
+
 def _line(args, metric, value, unit, ms_per_step, workload, extra, roofline, higher=True):
     line = {
         "metric": metric,
@@ -450,24 +474,24 @@ def bench_prefill(args, dev):
     splits = args.splits or ops.prefill_default_splits(16, HQ, HKV, D, maxe, maxs)
     ws = ops.prefill_workspace(16, t, maxe, HQ, HKV, D, splits, dev)
 
-    def run(i, ev):
-        layer = i % LAYERS
-        if ev:
-            ev[0].record()
+    def run_layer(layer):
+        if layer == 0:  # the work list depends only on the batch: built once per step
+            ops.prefill_plan(qi, ki, None, num_tokens=t, max_extend_len=maxe, max_seq_len=maxs, num_qo_heads=HQ,
+                             num_kv_heads=HKV, head_dim=D, dtype=torch.bfloat16, max_splits=splits, workspace=ws)
         ops.prefill_ragged_attention(q, kps[layer], vps[layer], qi, ki, kx, None, D**-0.5, max_extend_len=maxe,
-                                     max_seq_len=maxs, max_splits=splits, out=out, workspace=ws)
-        if ev:
-            ev[1].record()
+                                     max_seq_len=maxs, max_splits=splits, out=out, workspace=ws, planned=True)
 
-    sec, ev_s = _timed(args, run)
-    tflops = flops / ev_s / 1e12
-    gbs = nbytes / ev_s / 1e9
+    step = _b2b_step_time(args, run_layer, LAYERS)
+    sec = step / LAYERS  # one layer: attention + split-K merge (+ 1/28 of the plan)
+    tflops = flops / sec / 1e12
+    gbs = nbytes / sec / 1e9
     return _line(
         args, "ragged-prefill attention µs/layer, 16 requests over cached prefixes, Qwen3-0.6B heads",
-        sec * 1e6, "us", sec * 1e3,
+        sec * 1e6, "us", step * 1e3,
         "ragged chunked prefill, Qwen3-0.6B attention (16 q / 8 kv heads, head_dim 128); 16 requests, prefix "
         "U[0,4096], extend U[64,512] rescaled to <= 2048 packed tokens (seed 0), page_size 1, 131072-slot "
-        "bf16 pools of 28 layers in rotation; bottom-right causal",
+        "bf16 pools; one step = one work-list plan + the 28 layers back to back (median of steps), each layer "
+        "attention + split-K merge; bottom-right causal",
         {"requests": 16, "packed_tokens": t, "sum_prefix": int(case.prefix_lens.sum()), "max_splits": splits,
          "flops_per_step": flops, "bytes_per_step": nbytes, "tflops": round(tflops, 2),
          "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4)},
@@ -513,28 +537,8 @@ def bench_rope(args, dev):
         ops.rope(ks[layer], posd, inv, D, out=k_rot)
         ops.store_kv(k_rot, vs[layer], locd, kps[layer], vps[layer])
 
-    def step_time(fn):
-        """One step = the 28 layers' launches back to back: a spin kernel holds the
-        stream while the host enqueues them, so the events see GPU time only
-        (the host wrapper needs longer per call than one launch runs)."""
-        for i in range(args.warmup):
-            for layer in range(LAYERS):
-                fn(layer)
-        torch.cuda.synchronize()
-        times = []
-        for _ in range(args.steps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            torch.cuda._sleep(6_000_000)  # ~3 ms: longer than the host needs to enqueue a step
-            a.record()
-            for layer in range(LAYERS):
-                fn(layer)
-            b.record()
-            torch.cuda.synchronize()
-            times.append(a.elapsed_time(b) / 1e3)
-        return float(np.median(times))
-
-    sec = step_time(fused)
-    sec_unfused = step_time(unfused)
+    sec = _b2b_step_time(args, fused, LAYERS)
+    sec_unfused = _b2b_step_time(args, unfused, LAYERS)
     per_launch = sec / LAYERS
     gbs = nbytes / per_launch / 1e9
     return _line(

@@ -16,7 +16,7 @@
  *   msgl_paged_decode_store  kvcache/pool.py:47-50 + attention/metal.py:112-131 in one launch
  *                            (+ _plan / _planned / _store_planned: plan once per step)
  *   msgl_prefill_ragged      attention/base.py:85-105     BaseAttnBackend._forward_prefill
- *                            (+ _default_splits, _workspace_size)
+ *                            (+ _default_splits, _workspace_size; _plan / _planned: plan once per step)
  *   msgl_build_step_indices  scheduler/scheduler.py:154-157 + attention/metal.py:145-152
  *                            + attention/base.py:70-83 (index metadata, on the GPU)
  *   msgl_table_scatter       device mirror of scheduler/cache.py:53-72's page-table writes
@@ -205,6 +205,26 @@ int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, c
                         int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                         int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                         void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * The ragged prefill in two parts, for callers that run it once per layer over
+ * the same batch: msgl_prefill_plan writes the work list (which depends only
+ * on q_indptr, kv_indptr / seq_lens and the sizes) into the workspace, then
+ * msgl_prefill_ragged_planned (the arguments of msgl_prefill_ragged) runs the
+ * attention from it, skipping one launch per layer. Same workspace, sizes,
+ * dtype and max_splits in both calls, on one stream; fp32 has no work list
+ * (the plan is a no-op).
+ */
+int msgl_prefill_plan(const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_reqs,
+                      int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len, int32_t num_qo_heads,
+                      int32_t num_kv_heads, int32_t head_dim, int32_t dtype, int32_t max_splits, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+int msgl_prefill_ragged_planned(const void* q, const void* k_pool, const void* v_pool, const int32_t* q_indptr,
+                                const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                                int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                                int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
+                                void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Per-step index construction on the GPU from a device copy of the page table

@@ -86,7 +86,12 @@ struct PrefillParams {
   int items;    // (request, query block, chunk) triples x kv heads: the grid
   int plan_capacity;  // work items the plan area holds
   float scale_log2;
+  int mode;  // host side only: which launches a call makes (PrefillMode)
 };
+
+// Launches of one call: the work list and the attention (+ merge), only the
+// attention with a work list already in the workspace, or only the work list.
+enum PrefillMode { kPlanAndRun = 0, kRunPlanned = 1, kPlanOnly = 2 };
 
 __device__ __forceinline__ int64_t kv_slot(const PrefillParams& p, int start, int tok) {
   int64_t s;
@@ -885,8 +890,11 @@ int launch16(PrefillParams p, int max_e, hipStream_t stream) {
     set_error("msgl_prefill_ragged: workspace holds %d work items, %lld needed", p.plan_capacity, (long long)items);
     return MSGL_ERR_WORKSPACE;
   }
-  hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p, BQ);
-  MSGL_CHECK_LAUNCH("msgl_prefill_ragged (plan)");
+  if (p.mode != kRunPlanned) {
+    hipLaunchKernelGGL(prefill_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p, BQ);
+    MSGL_CHECK_LAUNCH("msgl_prefill_ragged (plan)");
+  }
+  if (p.mode == kPlanOnly) return MSGL_OK;
   const int grid = (int)items;
   static bool attr_set = false;  // per process; the attribute is per function
   if (Geo::LDS_BYTES > 65536 && !attr_set) {
@@ -921,6 +929,7 @@ int launch32(const PrefillParams& p, int max_e, hipStream_t stream) {
 template <typename T, int D, int G>
 int launch_prefill(const PrefillParams& p, int max_e, hipStream_t s) {
   if constexpr (sizeof(T) == 4) {
+    if (p.mode == kPlanOnly) return MSGL_OK;  // the fp32 path has no work list
     return launch32<D, G>(p, max_e, s);
   } else {
     return launch16<T, D, G>(p, max_e, s);
@@ -1004,33 +1013,33 @@ extern "C" int64_t msgl_prefill_workspace_size(int32_t num_reqs, int32_t num_tok
       .bytes;
 }
 
-extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, const int32_t* q_indptr,
-                                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
-                                   int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
-                                   int32_t num_qo_heads,
-                                   int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
-                                   int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
-                                   int64_t workspace_bytes, void* stream) {
+namespace {
+int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, const void* v_pool,
+                 const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                 const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
+                 int32_t max_seq_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                 int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                 int64_t workspace_bytes, void* stream) {
   using namespace msgl;
   clear_error();
-  MSGL_CHECK_ARG(num_reqs >= 0 && num_tokens >= 0 && max_extend_len >= 0, "msgl_prefill_ragged: sizes must be >= 0");
+  MSGL_CHECK_ARG(num_reqs >= 0 && num_tokens >= 0 && max_extend_len >= 0, "%s: sizes must be >= 0", fn);
   if (num_reqs == 0 || max_extend_len == 0 || num_tokens == 0) return MSGL_OK;
-  MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "msgl_prefill_ragged: sizes must be > 0");
-  MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "msgl_prefill_ragged: Hq (%d) must be a multiple of Hkv (%d)",
-                 num_qo_heads, num_kv_heads);
-  MSGL_CHECK_ARG(page_size >= 1, "msgl_prefill_ragged: page_size must be >= 1");
-  MSGL_CHECK_ARG(page_size == 1 || seq_lens != nullptr, "msgl_prefill_ragged: page_size > 1 needs seq_lens");
-  MSGL_CHECK_ARG(num_slots > 0 && num_slots <= ((int64_t)1 << 31) - 1,
-                 "msgl_prefill_ragged: num_slots must be in [1, 2^31)");
-  MSGL_CHECK_ARG(scale > 0.f && scale < INFINITY, "msgl_prefill_ragged: scale must be positive and finite");
-  MSGL_CHECK_ARG(max_splits >= 1 && max_splits <= kMaxSplits, "msgl_prefill_ragged: max_splits must be in [1, %d]",
-                 kMaxSplits);
-  MSGL_CHECK_ARG(q && k_pool && v_pool && q_indptr && kv_indptr && kv_indices && out,
-                 "msgl_prefill_ragged: null pointer");
-  MSGL_CHECK_ARG(((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) % 16 == 0,
-                 "msgl_prefill_ragged: q, pools and out must be 16-byte aligned");
+  MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "%s: sizes must be > 0", fn);
+  MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "%s: Hq (%d) must be a multiple of Hkv (%d)", fn, num_qo_heads,
+                 num_kv_heads);
+  MSGL_CHECK_ARG(max_splits >= 1 && max_splits <= kMaxSplits, "%s: max_splits must be in [1, %d]", fn, kMaxSplits);
+  MSGL_CHECK_ARG(q_indptr && kv_indptr, "%s: null pointer", fn);
+  if (mode != kPlanOnly) {
+    MSGL_CHECK_ARG(page_size >= 1, "%s: page_size must be >= 1", fn);
+    MSGL_CHECK_ARG(page_size == 1 || seq_lens != nullptr, "%s: page_size > 1 needs seq_lens", fn);
+    MSGL_CHECK_ARG(num_slots > 0 && num_slots <= ((int64_t)1 << 31) - 1, "%s: num_slots must be in [1, 2^31)", fn);
+    MSGL_CHECK_ARG(scale > 0.f && scale < INFINITY, "%s: scale must be positive and finite", fn);
+    MSGL_CHECK_ARG(q && k_pool && v_pool && kv_indices && out, "%s: null pointer", fn);
+    MSGL_CHECK_ARG(((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) % 16 == 0,
+                   "%s: q, pools and out must be 16-byte aligned", fn);
+  }
   if (dtype_size(dtype) == 0) {
-    set_error("msgl_prefill_ragged: unknown dtype %d", dtype);
+    set_error("%s: unknown dtype %d", fn, dtype);
     return MSGL_ERR_UNSUPPORTED;
   }
   PrefillParams p;
@@ -1062,16 +1071,17 @@ extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void
   p.nqb = 0;
   p.items = 0;
   p.scale_log2 = scale * kLog2eP;
+  p.mode = mode;
   if (dtype != MSGL_F32) {
     const PrefillWorkspace w =
         prefill_workspace(num_reqs, num_tokens, max_extend_len, num_qo_heads, num_kv_heads, head_dim, p.splits);
     if (workspace == nullptr || workspace_bytes < w.bytes) {
-      set_error("msgl_prefill_ragged: workspace of %lld bytes needed (%d splits), got %lld", (long long)w.bytes,
-                p.splits, (long long)workspace_bytes);
+      set_error("%s: workspace of %lld bytes needed (%d splits), got %lld", fn, (long long)w.bytes, p.splits,
+                (long long)workspace_bytes);
       return MSGL_ERR_WORKSPACE;
     }
-    MSGL_CHECK_ARG((uintptr_t)workspace % 256 == 0, "msgl_prefill_ragged: workspace must be 256-byte aligned");
-    MSGL_CHECK_ARG(w.items <= INT32_MAX, "msgl_prefill_ragged: too many work items");
+    MSGL_CHECK_ARG((uintptr_t)workspace % 256 == 0, "%s: workspace must be 256-byte aligned", fn);
+    MSGL_CHECK_ARG(w.items <= INT32_MAX, "%s: too many work items", fn);
     uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
     p.plan_count = reinterpret_cast<int*>(ws);
     p.plan = reinterpret_cast<int4*>(ws + w.plan);
@@ -1089,4 +1099,40 @@ extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void
     case MSGL_F16: return prefill_dim<f16_t>(p, max_extend_len, head_dim, group, s);
   }
   return MSGL_ERR_UNSUPPORTED;
+}
+}  // namespace
+
+extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, const int32_t* q_indptr,
+                                   const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                                   int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                   int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
+                                   void* workspace, int64_t workspace_bytes, void* stream) {
+  return prefill_impl("msgl_prefill_ragged", msgl::kPlanAndRun, q, k_pool, v_pool, q_indptr, kv_indptr, kv_indices,
+                      seq_lens, num_reqs, num_tokens, max_extend_len, max_seq_len, num_qo_heads, num_kv_heads,
+                      head_dim, page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes,
+                      stream);
+}
+
+extern "C" int msgl_prefill_ragged_planned(const void* q, const void* k_pool, const void* v_pool,
+                                           const int32_t* q_indptr, const int32_t* kv_indptr,
+                                           const int32_t* kv_indices, const int32_t* seq_lens, int32_t num_reqs,
+                                           int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                                           int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                           int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                                           int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
+                                           void* stream) {
+  return prefill_impl("msgl_prefill_ragged_planned", msgl::kRunPlanned, q, k_pool, v_pool, q_indptr, kv_indptr,
+                      kv_indices, seq_lens, num_reqs, num_tokens, max_extend_len, max_seq_len, num_qo_heads,
+                      num_kv_heads, head_dim, page_size, num_slots, dtype, scale, max_splits, out, workspace,
+                      workspace_bytes, stream);
+}
+
+extern "C" int msgl_prefill_plan(const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* seq_lens,
+                                 int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                                 int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                                 int32_t max_splits, void* workspace, int64_t workspace_bytes, void* stream) {
+  return prefill_impl("msgl_prefill_plan", msgl::kPlanOnly, nullptr, nullptr, nullptr, q_indptr, kv_indptr, nullptr,
+                      seq_lens, num_reqs, num_tokens, max_extend_len, max_seq_len, num_qo_heads, num_kv_heads,
+                      head_dim, 1, 1, dtype, 1.f, max_splits, nullptr, workspace, workspace_bytes, stream);
 }

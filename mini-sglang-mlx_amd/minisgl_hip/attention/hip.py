@@ -55,6 +55,7 @@ class HipPrefillDevice:
     num_tokens: int
     max_seq_len: int
     max_splits: int
+    workspace: Optional[torch.Tensor] = None  # this step's work list (planned once) and split-K partials
 
 
 class HipAttnBackend(BaseAttnBackend):
@@ -69,7 +70,6 @@ class HipAttnBackend(BaseAttnBackend):
         super().__init__(config, kv_cache, page_table)
         self.device = kv_cache.k[0].device
         self.fuse_decode_store = fuse_decode_store and hasattr(kv_cache, "take_pending")
-        self._workspace: Optional[torch.Tensor] = None
 
     def prepare_metadata(self, batch: "Batch") -> None:
         if self.fuse_decode_store:
@@ -103,14 +103,6 @@ class HipAttnBackend(BaseAttnBackend):
             max_splits=splits,
             workspace=ws,
         )
-
-    def _shared_workspace(self, need: int) -> Optional[torch.Tensor]:
-        if need == 0:
-            return None
-        if self._workspace is None or self._workspace.numel() < need:
-            # one buffer reused by every layer and step: launches run in stream order
-            self._workspace = torch.empty(need, dtype=torch.uint8, device=self.device)
-        return self._workspace
 
     def forward_decode(self, q: torch.Tensor, layer_id: int, meta: HipDecodeMetadata) -> torch.Tensor:
         ws = meta.workspace
@@ -156,10 +148,20 @@ class HipAttnBackend(BaseAttnBackend):
             max_splits=1,
         )
         cfg = self.config
-        if self.kv_cache.dtype != torch.float32:  # fp32 runs one pass per query block
+        if self.kv_cache.dtype != torch.float32:  # fp32 runs one pass per query block, with no work list
+            r = len(batch.reqs)
             dev.max_splits = ops.prefill_default_splits(
-                len(batch.reqs), cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, dev.max_extend_len, dev.max_seq_len
+                r, cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, dev.max_extend_len, dev.max_seq_len
             )
+            # a workspace per step (see prepare_decode); the work list is built once for all layers
+            dev.workspace = torch.empty(
+                ops.prefill_workspace_bytes(r, dev.num_tokens, dev.max_extend_len, cfg.num_qo_heads,
+                                            cfg.num_kv_heads, cfg.head_dim, dev.max_splits),
+                dtype=torch.uint8, device=self.device)
+            ops.prefill_plan(dev.q_indptr, dev.kv_indptr, dev.seq_lens, num_tokens=dev.num_tokens,
+                             max_extend_len=dev.max_extend_len, max_seq_len=dev.max_seq_len,
+                             num_qo_heads=cfg.num_qo_heads, num_kv_heads=cfg.num_kv_heads, head_dim=cfg.head_dim,
+                             dtype=self.kv_cache.dtype, max_splits=dev.max_splits, workspace=dev.workspace)
         return PrefillMetadata(
             last_indices=_to_device(np.array(q_offsets[1:], dtype=np.int32) - 1, self.device),
             q_offsets=q_offsets,
@@ -181,12 +183,6 @@ class HipAttnBackend(BaseAttnBackend):
             max_extend_len=d.max_extend_len,
             max_seq_len=d.max_seq_len,
             max_splits=d.max_splits,
-            workspace=self._shared_workspace(
-                ops.prefill_workspace_bytes(
-                    d.q_indptr.shape[0] - 1, d.num_tokens, d.max_extend_len, self.config.num_qo_heads,
-                    self.config.num_kv_heads, self.config.head_dim, d.max_splits,
-                )
-                if self.kv_cache.dtype != torch.float32
-                else 0
-            ),
+            workspace=d.workspace,
+            planned=d.workspace is not None,
         )

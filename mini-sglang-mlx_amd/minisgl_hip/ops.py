@@ -279,6 +279,7 @@ def prefill_ragged_attention(
     max_splits: Optional[int] = None,
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
+    planned: bool = False,
 ) -> torch.Tensor:
     """Ragged prefill over cached prefixes; counterpart of attention/base.py:85-105.
 
@@ -288,7 +289,8 @@ def prefill_ragged_attention(
     ``max_extend_len`` must bound every request's extend length (host-known);
     ``max_seq_len`` (max total length, 0 = unknown) only tunes the key-range
     split (its default and the chunk length). ``workspace`` (from ``prefill_workspace``) is allocated per
-    call when the split needs one and none large enough is given.
+    call when the split needs one and none large enough is given. With ``planned`` the workspace
+    already holds the work list ``prefill_plan`` built for these indices and sizes.
     """
     if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
         raise ValueError("q must be [T, Hq, D] and pools [N, Hkv, D]")
@@ -325,9 +327,12 @@ def prefill_ragged_attention(
     need = (prefill_workspace_bytes(num_reqs, t, int(max_extend_len), hq, hkv, d, max_splits)
             if q.dtype != torch.float32 else 0)
     if need > 0 and (workspace is None or workspace.numel() * workspace.element_size() < need):
+        if planned:
+            raise ValueError("planned prefill needs the workspace its plan was built in")
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    status = lib.msgl_prefill_ragged(
+    fn = lib.msgl_prefill_ragged_planned if planned else lib.msgl_prefill_ragged
+    status = fn(
         _lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool),
         _lib.ptr(q_indptr), _lib.ptr(kv_indptr), _lib.ptr(kv_indices), _lib.ptr(seq_lens),
         num_reqs, t, int(max_extend_len), int(max_seq_len), hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
@@ -335,6 +340,35 @@ def prefill_ragged_attention(
     )
     _lib.check(status, "msgl_prefill_ragged")
     return out
+
+
+def prefill_plan(
+    q_indptr: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    seq_lens: Optional[torch.Tensor],
+    *,
+    num_tokens: int,
+    max_extend_len: int,
+    max_seq_len: int,
+    num_qo_heads: int,
+    num_kv_heads: int,
+    head_dim: int,
+    dtype: torch.dtype,
+    max_splits: int,
+    workspace: torch.Tensor,
+) -> None:
+    """Build the ragged prefill's work list into ``workspace`` once for a batch;
+    every layer then calls ``prefill_ragged_attention(..., planned=True)`` with
+    the same indices, sizes and workspace."""
+    dev = workspace.device
+    for name, x in (("q_indptr", q_indptr), ("kv_indptr", kv_indptr), ("seq_lens", seq_lens)):
+        _check_index(name, x, dev)
+    status = _lib.load().msgl_prefill_plan(
+        _lib.ptr(q_indptr), _lib.ptr(kv_indptr), _lib.ptr(seq_lens), q_indptr.shape[0] - 1, int(num_tokens),
+        int(max_extend_len), int(max_seq_len), num_qo_heads, num_kv_heads, head_dim, _lib.dtype_code(dtype),
+        int(max_splits), _lib.ptr(workspace), workspace.numel() * workspace.element_size(), _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_prefill_plan")
 
 
 def build_step_indices(

@@ -105,6 +105,13 @@ def test_host_side_argument_errors():
     assert pf(4, 0, dtype=0, d=96) == _lib.MSGL_ERR_UNSUPPORTED  # fp32 needs no workspace: reaches dispatch
     assert lib.msgl_prefill_ragged(nul, nul, nul, nul, nul, nul, nul, 0, 0, 0, 0, 16, 8, 128, 1, 100, 1, 0.1, 1,
                                    nul, nul, 0, nul) == _lib.MSGL_OK
+    # prefill plan: (q_indptr, kv_indptr, seq_lens, R, T, maxE, maxL, Hq, Hkv, D, dtype, splits, ws, ws_bytes, stream)
+    pp = lambda splits=2, ws_bytes=1 << 20, dtype=1: lib.msgl_prefill_plan(  # noqa: E731
+        16, 16, nul, 2, 64, 32, 0, 16, 8, 128, dtype, splits, 256, ws_bytes, nul)
+    assert pp(splits=0) == _lib.MSGL_ERR_INVALID and "max_splits" in _lib.last_error()
+    assert pp(ws_bytes=0) == _lib.MSGL_ERR_WORKSPACE
+    assert pp(dtype=0, ws_bytes=0) == _lib.MSGL_OK  # fp32 has no work list
+    assert lib.msgl_prefill_plan(nul, nul, nul, 0, 0, 0, 0, 16, 8, 128, 1, 1, nul, 0, nul) == _lib.MSGL_OK
     # step indices: (table, rows, stride, table_idx, cached, device_len, R, page, q_indptr, positions, out_loc,
     #                last, token_cap, kv_indptr, kv_indices, kv_cap, stream)
     bi = lambda R, page=1, rows_=4, stride=64, tok_out=16, kv_out=16: lib.msgl_build_step_indices(  # noqa: E731

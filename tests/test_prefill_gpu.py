@@ -130,3 +130,29 @@ def test_prefill_splits_page16(cuda_device):
     q, kn, vn, kp, vp, out = _run(case, 32, 8, 128, torch.bfloat16, cuda_device, 50, page_size=16)
     ref = _oracle(case, q, kn, vn, kp, vp, 128)
     assert_close(out, ref, torch.bfloat16, "prefill splits page16")
+
+
+def test_planned_matches_unplanned(cuda_device):
+    """A work list built once (msgl_prefill_plan) and reused by the planned call
+    gives the self-planning call's result bit for bit, over several layers' pools."""
+    case = workloads.prefill_case(16, 4096, 64, 512, 2048, num_slots=1 << 17, seed=0)
+    dt = torch.bfloat16
+    t = case.num_tokens
+    q = randn((t, 16, 128), 90, dt).to(cuda_device)
+    qi, ki = i32(case.q_indptr, cuda_device), i32(case.kv_indptr, cuda_device)
+    kx = i32(case.kv_indices, cuda_device)
+    maxe, maxs = int(case.extend_lens.max()), int(case.seq_lens.max())
+    splits = ops.prefill_default_splits(16, 16, 8, 128, maxe, maxs)
+    ws = ops.prefill_workspace(16, t, maxe, 16, 8, 128, splits, cuda_device)
+    ops.prefill_plan(qi, ki, None, num_tokens=t, max_extend_len=maxe, max_seq_len=maxs, num_qo_heads=16,
+                     num_kv_heads=8, head_dim=128, dtype=dt, max_splits=splits, workspace=ws)
+    for layer in range(3):
+        kp = randn((1 << 17, 8, 128), 91 + layer, dt).to(cuda_device)
+        vp = randn((1 << 17, 8, 128), 95 + layer, dt).to(cuda_device)
+        print(f"case prefill planned layer={layer}", flush=True)
+        a = ops.prefill_ragged_attention(q, kp, vp, qi, ki, kx, None, 128**-0.5, max_extend_len=maxe,
+                                         max_seq_len=maxs, max_splits=splits)
+        b = ops.prefill_ragged_attention(q, kp, vp, qi, ki, kx, None, 128**-0.5, max_extend_len=maxe,
+                                         max_seq_len=maxs, max_splits=splits, workspace=ws, planned=True)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b), f"layer {layer}"
