@@ -59,7 +59,12 @@ namespace {
 
 constexpr float kLog2eP = 1.4426950408889634f;
 constexpr int KT = 32;           // keys per tile
-constexpr int NWAVE = 4;         // wavefronts per workgroup
+constexpr int NWAVE = 4;         // wavefronts per workgroup (fp32 kernel)
+#ifndef MSGL_PREFILL_WAVES
+#define MSGL_PREFILL_WAVES 4
+#endif
+constexpr int NWAVE16 = MSGL_PREFILL_WAVES;  // wavefronts per workgroup of the 16-bit kernel
+constexpr int THREADS16 = NWAVE16 * 64;
 constexpr int kWin = 1024;       // keys whose slots are staged in LDS at a time
 constexpr int kMinChunk = 256;   // smallest key range given its own workgroup
 constexpr int kMaxSplits = 16;
@@ -155,6 +160,23 @@ __device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
   asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory");
 }
 
+// The value of lane l ^ 32 combined with this lane's, on the VALU:
+// v_permlane32_swap of x with itself leaves (x[l % 32], x[l % 32 + 32]) in
+// every lane (checked on gfx950), so max / sum of the pair needs no LDS
+// round trip as a lane shuffle would.
+__device__ __forceinline__ f32x2_t halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return f32x2_t{__uint_as_float(r[0]), __uint_as_float(r[1])};
+}
+__device__ __forceinline__ float xor32_max(float x) {
+  const f32x2_t h = halves(x);
+  return fmaxf(h[0], h[1]);
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const f32x2_t h = halves(x);
+  return h[0] + h[1];
+}
+
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -200,7 +222,7 @@ struct MMA32<f16_t> {
 // Geometry of the 16-bit kernel for one head_dim.
 template <int D>
 struct G16 {
-  static constexpr int ROWS = NWAVE * 32;          // query rows per workgroup (32 per wavefront)
+  static constexpr int ROWS = NWAVE16 * 32;        // query rows per workgroup (32 per wavefront)
   static constexpr int RBYTES = D * 2;              // bytes per K/V row
   static constexpr int CPR = D / 8;                 // 16-byte chunks per row
   static constexpr int SWZ = CPR >= 16 ? 15 : CPR - 1;
@@ -211,9 +233,10 @@ struct G16 {
   // one at 256 (132 KiB, 512 VGPRs).
   static constexpr int NS = 4;  // V of tile t-1, tiles t and t+1 resident, tile t+2 in flight
   static constexpr int WAVES = D <= 128 ? 2 : 1;
-  static constexpr int IPW = TILE_BYTES / 1024 / NWAVE;  // 1 KiB transfers per wavefront, each of K and V
+  static constexpr int NXFER = TILE_BYTES / 1024;                // 1 KiB transfers per tile, each of K and V
+  static constexpr int IPW = (NXFER + NWAVE16 - 1) / NWAVE16;     // of them per wavefront (all or none)
   static constexpr int LDS_BYTES = NS * STAGE_BYTES + kWin * 4;
-  static_assert(TILE_BYTES % (1024 * NWAVE) == 0, "a tile must split evenly over the wavefronts");
+  static_assert(NXFER % NWAVE16 == 0 || NXFER < NWAVE16, "a tile must split evenly over the wavefronts");
 };
 
 // XOR swizzle of a row's 16-byte chunks: a bijection on r % 16, so 16
@@ -236,7 +259,7 @@ __device__ __forceinline__ void sched_interleave() {
 }
 
 template <typename T, int D, int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAVES))) void prefill16_kernel(
+__global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D>::WAVES))) void prefill16_kernel(
     PrefillParams p) {
   using Geo = G16<D>;
   constexpr int ROWS = Geo::ROWS;
@@ -321,7 +344,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAV
   const uint8_t* kcol[IPW];
 #pragma unroll
   for (int i = 0; i < IPW; ++i) {
-    const int flat = (wave + NWAVE * i) * 64 + lane;
+    const int flat = (wave + NWAVE16 * i) * 64 + lane;
     dma_row[i] = flat / CPR;
     kcol[i] = kp + head_off + (((flat % CPR) ^ (swz(dma_row[i]) & SWZ)) << 4);
   }
@@ -335,9 +358,11 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAV
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
       const uint8_t* g = kcol[i] + (int64_t)nslot[i] * row_stride;
-      const uint32_t lk = __builtin_amdgcn_readfirstlane(sb + (wave + NWAVE * i) * 1024);
-      dma16(g, lk);
-      dma16(g + vk, lk + Geo::TILE_BYTES);
+      if (wave + NWAVE16 * i < Geo::NXFER) {  // wave-uniform: a wavefront issues all its transfers or none
+        const uint32_t lk = __builtin_amdgcn_readfirstlane(sb + (wave + NWAVE16 * i) * 1024);
+        dma16(g, lk);
+        dma16(g + vk, lk + Geo::TILE_BYTES);
+      }
     }
   };
   // Wait until this wavefront's transfers of a tile have landed, `after`
@@ -476,7 +501,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAV
     const int ntiles = (nw + KT - 1) / KT;
     const int kend = w0 + nw;
     __syncthreads();  // every wavefront is done with the previous window
-    for (int i = tid; i < nw; i += 256) slots[i] = (int)kv_slot(p, kv_start, w0 + i);
+    for (int i = tid; i < nw; i += THREADS16) slots[i] = (int)kv_slot(p, kv_start, w0 + i);
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < 2; ++s)
@@ -510,7 +535,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAV
         mloc = rowmax_masked(s_cur, x, kbase, kend);
         sched_interleave<NQF, NQF, 4>();
       }
-      mloc = fmaxf(mloc, __shfl_xor(mloc, 32));  // the row's other 16 keys
+      mloc = xor32_max(mloc);  // with the row's other 16 keys
       // B
       rescale(mloc, pa_prev, !FIRST);
       // C
@@ -529,7 +554,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(G16<D>::WAV
   }
 
   // ---- results: accumulator i is WG row wave*32 + 8(i/4) + 4h + i%4, column 32dt + rl ----
-  const float l_row = l_run + __shfl_xor(l_run, 32);  // both halves of this lane's row
+  const float l_row = xor32_sum(l_run);  // both halves of this lane's row
   if (nchunks == 1) {
     const float inv = 1.f / l_row;
     T* out = reinterpret_cast<T*>(p.out);
@@ -877,7 +902,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
 // ---------------------------------------------------------------------------
 // launch
 // ---------------------------------------------------------------------------
-int tokens_per_block16(int group) { return NWAVE * 32 / group; }
+int tokens_per_block16(int group) { return NWAVE16 * 32 / group; }
 
 template <typename T, int D, int G>
 int launch16(PrefillParams p, int max_e, hipStream_t stream) {
@@ -905,7 +930,7 @@ int launch16(PrefillParams p, int max_e, hipStream_t stream) {
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((prefill16_kernel<T, D, G>), dim3(grid), dim3(256), Geo::LDS_BYTES, stream, p);
+  hipLaunchKernelGGL((prefill16_kernel<T, D, G>), dim3(grid), dim3(THREADS16), Geo::LDS_BYTES, stream, p);
   MSGL_CHECK_LAUNCH("msgl_prefill_ragged");
   if (p.splits > 1) {
     constexpr int HPB = 256 / (D / 4);
