@@ -605,7 +605,8 @@ def bench_mixed(args, dev):
         sec * 1e6, "us", sec * 1e3,
         "one step, Qwen3-8B attention (32 q / 8 kv heads, head_dim 128), one layer, page_size 16, 8M-slot bf16 "
         "pool: 128 decode requests (context U[512,32768], seed 0) + 2 prefill chunks of 1024 over prefixes "
-        "0 and 8192; indices built on the GPU from a req_to_token table",
+        "0 and 8192; indices built on the GPU from a req_to_token table; the prefill on a second stream "
+        "concurrent with the decode",
         {"decode_requests": nd, "decode_sum_context": int(dec_lens.sum()), "prefill_tokens": int(ext.sum()),
          "decode_bytes": dec_bytes, "prefill_flops": pf_flops, "prefill_bytes": pf_bytes,
          "store_bytes": store_bytes, "decode_splits": step.decode_splits, "prefill_splits": step.prefill_splits,

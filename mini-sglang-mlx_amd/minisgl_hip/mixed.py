@@ -14,6 +14,12 @@ scheduler that does mix them pays one metadata build per step:
 Decode requests come first in the packed batch (one token each), prefill
 requests after them; q and out are the packed [T, Hq, D] tensors. Per request
 the results are those of the reference's decode or prefill path.
+
+Steps 3 and 4 touch disjoint output rows and pool rows no other part writes,
+so with ``concurrent`` (the default) the prefill runs on a second stream of
+default priority, forked after step 2 and joined before ``run`` returns: the
+HBM-bound decode and the matrix-core-bound prefill then share the GPU instead
+of running one after the other.
 """
 
 from __future__ import annotations
@@ -79,6 +85,7 @@ class MixedStep:
             else None
         )
         self.indices: Optional[dict] = None
+        self._side: Optional[torch.cuda.Stream] = None
 
     def build_indices(self) -> dict:
         self.indices = ops.build_step_indices(
@@ -87,22 +94,43 @@ class MixedStep:
         )
         return self.indices
 
-    def run(self, q, k_new, v_new, k_pool, v_pool, out, scale: float) -> torch.Tensor:
+    def run(self, q, k_new, v_new, k_pool, v_pool, out, scale: float, concurrent: bool = True) -> torch.Tensor:
         """q, k_new, v_new, out: packed [T, H, D]; the pools are one layer's."""
         idx = self.build_indices()
         nd = self.num_decode
-        if self.num_tokens > nd:
+        has_prefill = self.num_tokens > nd
+        if has_prefill:
             ops.store_kv(k_new[nd:], v_new[nd:], idx["out_loc"][nd:], k_pool, v_pool)
+
+        def prefill():
+            ops.prefill_ragged_attention(
+                q, k_pool, v_pool, idx["q_indptr"][nd:], idx["kv_indptr"][nd:], idx["kv_indices"],
+                self.device_len[nd:], scale, max_extend_len=self.max_chunk, max_seq_len=self.max_seq_len,
+                page_size=self.page_size, max_splits=self.prefill_splits, out=out, workspace=self.prefill_ws,
+            )
+
+        joined = None
+        if has_prefill and nd and concurrent:
+            main = torch.cuda.current_stream(q.device)
+            if self._side is None:
+                self._side = torch.cuda.Stream(device=q.device)  # default priority
+            side = self._side
+            side.wait_stream(main)  # indices and the prefill rows' store are done
+            with torch.cuda.stream(side):
+                prefill()
+            for t in idx.values():  # this step's index tensors now also live on the side stream
+                t.record_stream(side)
+            joined = side
+        elif has_prefill and not nd:
+            prefill()
         if nd:
             ops.paged_decode_attention(
                 q[:nd], k_pool, v_pool, idx["kv_indptr"][: nd + 1], idx["kv_indices"], scale,
                 seq_lens=self.device_len[:nd], page_size=self.page_size, max_splits=self.decode_splits,
                 out=out[:nd], workspace=self.decode_ws, new_kv=(k_new[:nd], v_new[:nd], idx["out_loc"][:nd]),
             )
-        if self.num_tokens > nd:
-            ops.prefill_ragged_attention(
-                q, k_pool, v_pool, idx["q_indptr"][nd:], idx["kv_indptr"][nd:], idx["kv_indices"],
-                self.device_len[nd:], scale, max_extend_len=self.max_chunk, max_seq_len=self.max_seq_len,
-                page_size=self.page_size, max_splits=self.prefill_splits, out=out, workspace=self.prefill_ws,
-            )
+        if joined is not None:
+            torch.cuda.current_stream(q.device).wait_stream(joined)
+        elif has_prefill and nd:
+            prefill()
         return out

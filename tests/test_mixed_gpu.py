@@ -98,8 +98,11 @@ def test_mixed_step_full_size(cuda_device):
     step.run(q, kn, vn, kp, vp, out, SCALE)
     out2 = torch.empty_like(q)
     step.run(q, kn, vn, kp, vp, out2, SCALE)
+    out3 = torch.empty_like(q)
+    step.run(q, kn, vn, kp, vp, out3, SCALE, concurrent=False)  # decode, then prefill, on one stream
     torch.cuda.synchronize()
     assert torch.equal(out, out2), "mixed step is not deterministic"
+    assert torch.equal(out, out3), "the two-stream step differs from the one-stream order"
     longest = int(np.argmax(case.device_len[: case.num_decode]))
     for i in sorted({0, 5, longest, case.num_decode - 1}):
         _check_request(case, i, q, kp, vp, out)
