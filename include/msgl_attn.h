@@ -23,7 +23,8 @@
  *   msgl_rope                layers.py:45-56 (RotaryEmbedding.__call__, rotate-half mx.fast.rope)
  *   msgl_rope_store_kv       layers.py:107-109 (rotate q and k, then store_kv) in one launch
  *   msgl_store_kv_fp8,       the fp8 KV cache of docs/09-exercises.md:81-82 (store_kv and paged
- *   msgl_paged_decode_fp8    decode over pools of e4m3 codes with one scale per slot and kv head)
+ *   msgl_paged_decode_fp8,   decode over pools of e4m3 codes with one scale per slot and kv head,
+ *   msgl_prefill_ragged_fp8  and the ragged prefill over them)
  *
  * Layouts (identical to the reference, no transposes at the boundary):
  *   q, out   [T, Hq, D]   row-major, dtype `dtype`
@@ -321,6 +322,28 @@ int msgl_paged_decode_fp8_planned(const void* q, const void* k_pool, const void*
                                   int32_t head_dim, int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
                                   int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
                                   void* stream);
+
+/*
+ * msgl_prefill_ragged over fp8 pools (the same kv_scale [num_slots, Hkv, 2]
+ * layout): K tiles are widened to the query type for the matrix core and each
+ * key's K scale multiplies its score, V rows are read transposed as bytes and
+ * widened, and each key's V scale folds into its softmax weight. q/out bf16 or
+ * fp16; the workspace, default splits and msgl_prefill_plan are those of the
+ * unquantised prefill.
+ */
+int msgl_prefill_ragged_fp8(const void* q, const void* k_pool, const void* v_pool, const float* kv_scale,
+                            const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                            const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
+                            int32_t max_seq_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                            int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                            void* out, void* workspace, int64_t workspace_bytes, void* stream);
+int msgl_prefill_ragged_fp8_planned(const void* q, const void* k_pool, const void* v_pool, const float* kv_scale,
+                                    const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                                    const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens,
+                                    int32_t max_extend_len, int32_t max_seq_len, int32_t num_qo_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                                    int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                                    int64_t workspace_bytes, void* stream);
 
 #ifdef __cplusplus
 }

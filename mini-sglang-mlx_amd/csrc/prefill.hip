@@ -73,6 +73,7 @@ struct PrefillParams {
   const void* q;
   const void* k_pool;
   const void* v_pool;
+  const float* kv_scale;  // fp8 pools: [num_slots, Hkv, 2] (K, V) scales, else null
   const int32_t* q_indptr;
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
@@ -177,6 +178,39 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return h[0] + h[1];
 }
 
+// 4 bytes per active lane from global memory into LDS at m0 + 4 * lane.
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr) : "memory");
+}
+
+// ds_read_b64_tr_b8: within each 16-lane group, lane i receives byte i%8 of
+// source lanes i/8 + 2e at position e (e = 0..7; lane layout measured on
+// gfx950). If source lane s points at row key(s/2), columns c0 + 8(s%2) ..+7,
+// lane i receives rows key(0..7) of column c0 + i.
+__device__ __forceinline__ uint2 lds_read_tr8(const uint8_t* p) {
+  typedef int v2i __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr8_b64_v2i32((MSGL_LDS v2i*)(p)));
+}
+
+// 8 fp8 e4m3 values -> the 16-bit MFMA operand (exact: every e4m3 value is a
+// bf16 and an fp16 value).
+template <typename T>
+__device__ __forceinline__ u32x4 fp8x8(uint32_t w0, uint32_t w1);
+template <>
+__device__ __forceinline__ u32x4 fp8x8<bf16_t>(uint32_t w0, uint32_t w1) {
+  return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+}
+template <>
+__device__ __forceinline__ u32x4 fp8x8<f16_t>(uint32_t w0, uint32_t w1) {
+  return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
+}
+
 template <int N>
 __device__ __forceinline__ void vm_wait() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
@@ -219,15 +253,18 @@ struct MMA32<f16_t> {
   }
 };
 
-// Geometry of the 16-bit kernel for one head_dim.
-template <int D>
+// Geometry of the 16-bit kernel for one head_dim and pool element size KB
+// (2: bf16/fp16 pools; 1: fp8 pools, whose stages also hold the tile's scales).
+template <int D, int KB = 2>
 struct G16 {
   static constexpr int ROWS = NWAVE16 * 32;        // query rows per workgroup (32 per wavefront)
-  static constexpr int RBYTES = D * 2;              // bytes per K/V row
-  static constexpr int CPR = D / 8;                 // 16-byte chunks per row
+  static constexpr int RBYTES = D * KB;             // bytes per K/V row
+  static constexpr int CPR = RBYTES / 16;           // 16-byte chunks per row
   static constexpr int SWZ = CPR >= 16 ? 15 : CPR - 1;
   static constexpr int TILE_BYTES = KT * RBYTES;    // K (or V) tile
-  static constexpr int STAGE_BYTES = 2 * TILE_BYTES;
+  static constexpr int SCALE_BYTES = KB == 1 ? KT * 8 : 0;  // (K, V) scale of each key
+  static constexpr int STAGE_BYTES = 2 * TILE_BYTES + SCALE_BYTES;
+  static constexpr int SPW = 2 * KT / NWAVE16;      // scale dwords each wavefront transfers per tile
   // The occupancy the register budget is built for: two workgroups per CU at
   // head_dim <= 128 (LDS: 2 x 68 KiB of the 160 KiB at 128; <= 256 VGPRs),
   // one at 256 (132 KiB, 512 VGPRs).
@@ -237,6 +274,7 @@ struct G16 {
   static constexpr int IPW = (NXFER + NWAVE16 - 1) / NWAVE16;     // of them per wavefront (all or none)
   static constexpr int LDS_BYTES = NS * STAGE_BYTES + kWin * 4;
   static_assert(NXFER % NWAVE16 == 0 || NXFER < NWAVE16, "a tile must split evenly over the wavefronts");
+  static_assert(KB == 2 || (2 * KT) % NWAVE16 == 0, "a tile's scales must split evenly over the wavefronts");
 };
 
 // XOR swizzle of a row's 16-byte chunks: a bijection on r % 16, so 16
@@ -258,10 +296,13 @@ __device__ __forceinline__ void sched_interleave() {
   }
 }
 
-template <typename T, int D, int G>
+// KV: the pools' storage type, T itself or fp8e4m3 (codes plus the per-slot,
+// per-kv-head (K, V) scales of p.kv_scale).
+template <typename T, typename KV, int D, int G>
 __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D>::WAVES))) void prefill16_kernel(
     PrefillParams p) {
-  using Geo = G16<D>;
+  constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
+  using Geo = G16<D, (int)sizeof(KV)>;
   constexpr int ROWS = Geo::ROWS;
   static_assert(ROWS % G == 0, "group must divide the row block");
   constexpr int BQ = ROWS / G;  // query tokens per workgroup
@@ -312,7 +353,7 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
   u32x4 qf[NQF];
   {
     const uint8_t* qrow =
-        reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + my_tok) * p.hq + kvh * G + my_row % G) * RBYTES;
+        reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + my_tok) * p.hq + kvh * G + my_row % G) * D * 2;
 #pragma unroll
     for (int j = 0; j < NQF; ++j) qf[j] = ld16(qrow + (16 * j + 8 * h) * 2);
   }
@@ -349,29 +390,42 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
     kcol[i] = kp + head_off + (((flat % CPR) ^ (swz(dma_row[i]) & SWZ)) << 4);
   }
   const int64_t vk = vp - kp;  // V rows sit at the same offsets in the V pool
+  // a wavefront issues all its row transfers of a tile or none (wave-uniform)
+  const bool kv_issuer = Geo::NXFER >= NWAVE16 || wave < Geo::NXFER;
+  // fp8: lane j < SPW of wavefront w moves scale dword d = SPW w + j of the
+  // tile's [K scales of its KT keys | V scales]: (K or V = d / KT, key d % KT)
+  const int sc_dw = wave * Geo::SPW + lane;
+  const float* sc_src = Q8 ? p.kv_scale + (int64_t)kvh * 2 + sc_dw / KT : nullptr;
+  int sslot = 0;
   auto load_slots = [&](int t, int nw) {
 #pragma unroll
     for (int i = 0; i < IPW; ++i) nslot[i] = slots[min(t * KT + dma_row[i], nw - 1)];
+    if (Q8) sslot = slots[min(t * KT + sc_dw % KT, nw - 1)];
   };
   auto issue = [&](int st) {
     const uint32_t sb = lds0 + st * Geo::STAGE_BYTES;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
       const uint8_t* g = kcol[i] + (int64_t)nslot[i] * row_stride;
-      if (wave + NWAVE16 * i < Geo::NXFER) {  // wave-uniform: a wavefront issues all its transfers or none
+      if (kv_issuer) {
         const uint32_t lk = __builtin_amdgcn_readfirstlane(sb + (wave + NWAVE16 * i) * 1024);
         dma16(g, lk);
         dma16(g + vk, lk + Geo::TILE_BYTES);
       }
     }
+    if (Q8 && lane < Geo::SPW)  // one transfer per wavefront and tile, SPW lanes active
+      dma4(sc_src + (int64_t)sslot * p.hkv * 2,
+           __builtin_amdgcn_readfirstlane(sb + 2 * Geo::TILE_BYTES + wave * Geo::SPW * 4));
   };
   // Wait until this wavefront's transfers of a tile have landed, `after`
   // (0 or 1) tiles having been issued behind it.
   auto wait_tile = [&](int after) {
     if (after <= 0) {
       vm_wait<0>();
+    } else if (kv_issuer) {
+      vm_wait<2 * IPW + (Q8 ? 1 : 0)>();
     } else {
-      vm_wait<2 * IPW>();
+      vm_wait<Q8 ? 1 : 0>();
     }
   };
 
@@ -388,29 +442,48 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
       for (int i = 0; i < 16; ++i) s2[c][i] = 0.f;
 #pragma unroll
     for (int j = 0; j < NQF; ++j) {
-      const u32x4 a = *reinterpret_cast<const u32x4*>(krow + (((2 * j + h) ^ sw) << 4));
+      u32x4 a;
+      if constexpr (Q8) {  // d 16j + 8h .. +7 = half h of chunk j
+        const uint2 k8 = *reinterpret_cast<const uint2*>(krow + ((j ^ sw) << 4) + 8 * h);
+        a = fp8x8<T>(k8.x, k8.y);
+      } else {
+        a = *reinterpret_cast<const u32x4*>(krow + (((2 * j + h) ^ sw) << 4));
+      }
       s2[j & 1] = MMA32<T>::mma(a, qf[j], s2[j & 1]);
     }
     sdst = s2[0] + s2[1];
   };
   // Row max of the scores of tile t (keys kbase..), raw (scale > 0, so the raw
   // max orders like the scaled one); x gets the scores, -inf where masked.
-  auto rowmax_full = [&](const f32x16& sc, float (&x)[16]) {
+  // fp8: the K (which = 0) or V (1) scales of this lane's 16 keys 8c + 4h + r
+  // of the tile in ring stage st (four consecutive keys per c: one 16-byte read)
+  auto tile_scales = [&](int st, int which, float (&sc)[16]) {
+    const f32x4* sp =
+        reinterpret_cast<const f32x4*>(smem + st * Geo::STAGE_BYTES + 2 * Geo::TILE_BYTES + which * KT * 4);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f32x4 a = sp[2 * c + h];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) sc[4 * c + r] = a[r];
+    }
+  };
+  // (a quantised key's scale multiplies its score; ks is unused otherwise)
+  auto rowmax_full = [&](const f32x16& sc, const float (&ks)[16], float (&x)[16]) {
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      x[i] = sc[i];
+      x[i] = Q8 ? sc[i] * ks[i] : sc[i];
       m = fmaxf(m, x[i]);
     }
     return m;
   };
-  auto rowmax_masked = [&](const f32x16& sc, float (&x)[16], int kbase, int kend) {
+  auto rowmax_masked = [&](const f32x16& sc, const float (&ks)[16], float (&x)[16], int kbase, int kend) {
     // key 8(i/4) + 4h + i%4 of the tile is visible iff it is <= thr
     const int thr = min(limit, kend - 1) - kbase - 4 * h;
     float m = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-      x[i] = 8 * (i >> 2) + (i & 3) <= thr ? sc[i] : -INFINITY;
+      x[i] = 8 * (i >> 2) + (i & 3) <= thr ? (Q8 ? sc[i] * ks[i] : sc[i]) : -INFINITY;
       m = fmaxf(m, x[i]);
     }
     return m;
@@ -418,7 +491,8 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
   // P = exp2(x * scale - m_run) into the A operands of the two 16-key steps of
   // O += P V: slot (h, e) of step ks = key 16ks + 8(e/4) + 4h + e%4, i.e. this
   // lane's scores 8ks .. 8ks+7 in order
-  auto probs = [&](const float (&x)[16], u32x4 (&pa)[2]) {
+  // (fp8: a quantised V row's scale folds into its weight in P; l keeps the plain weights)
+  auto probs = [&](const float (&x)[16], const float (&vs)[16], u32x4 (&pa)[2]) {
     const float m_use = m_run == -INFINITY ? 0.f : m_run;  // a row may see nothing yet
     float pr[16];
     float lsum = 0.f;
@@ -428,6 +502,10 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
       lsum += pr[i];
     }
     l_run += lsum;
+    if (Q8) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) pr[i] *= vs[i];
+    }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -470,6 +548,24 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
     // .. +3 = logical chunk 4dt + 2(g%2) + (i16%4)/2, half i16%2
     const int i16 = lane & 15;
     const int gs = (lane >> 4) & 1;
+    if constexpr (Q8) {
+      // fp8: one transposing 8-bit read per (ks, dt). Source lane s = i16 reads
+      // row 16ks + 8(s/8) + 4h + (s/2)%4 (the key of slot e = s/2), columns
+      // 32dt + 16(g%2) + 8(s%2) .. +7 = half s%2 of logical chunk 2dt + g%2;
+      // lane i then holds that slot order for column 32dt + 16(g%2) + i.
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const int r = 16 * ks + 8 * (i16 >> 3) + 4 * h + ((i16 >> 1) & 3);
+        const uint8_t* vr = Vb + r * RBYTES + ((i16 & 1) << 3);
+        const int sw = swz(r) & SWZ;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) {
+          const uint2 v8 = lds_read_tr8(vr + (((2 * dt + gs) ^ sw) << 4));
+          acc[dt] = MMA32<T>::mma(pa[ks], fp8x8<T>(v8.x, v8.y), acc[dt]);
+        }
+      }
+      return;
+    }
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
       const int r0 = 16 * ks + 4 * h + (i16 >> 2);
@@ -525,15 +621,18 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
       // A (past the last tile, scores reads a stage whose transfers have all landed; unused)
       f32x16 s_next;
       float x[16];
+      float ksc[16];  // fp8: tile t's K scales
+      if constexpr (Q8) tile_scales(t % NS, 0, ksc);
+      constexpr int ADS = Q8 ? NQF + 4 : NQF;  // LDS reads of block A
       float mloc;
       if (kbase + KT <= kend && kbase + KT - 1 <= lim_lo) {
         scores((t + 1) % NS, s_next);
-        mloc = rowmax_full(s_cur, x);
-        sched_interleave<NQF, NQF, 2>();
+        mloc = rowmax_full(s_cur, ksc, x);
+        sched_interleave<ADS, NQF, 2>();
       } else {
         scores((t + 1) % NS, s_next);
-        mloc = rowmax_masked(s_cur, x, kbase, kend);
-        sched_interleave<NQF, NQF, 4>();
+        mloc = rowmax_masked(s_cur, ksc, x, kbase, kend);
+        sched_interleave<ADS, NQF, 4>();
       }
       mloc = xor32_max(mloc);  // with the row's other 16 keys
       // B
@@ -541,9 +640,12 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
       // C
       u32x4 pa_new[2];
       if constexpr (!FIRST) pv((t - 1) % NS, pa_prev);
-      probs(x, pa_new);
+      float vsc[16];  // fp8: tile t's V scales
+      if constexpr (Q8) tile_scales(t % NS, 1, vsc);
+      probs(x, vsc, pa_new);
       load_slots(t + 3, nw);  // for the next iteration's issue (clamped: harmless when unused)
-      if constexpr (!FIRST) sched_interleave<4 * NDT + IPW, 2 * NDT, 6>();
+      constexpr int CDS = Q8 ? 2 * NDT + IPW + 1 + 4 : 4 * NDT + IPW;  // LDS reads of block C
+      if constexpr (!FIRST) sched_interleave<CDS, 2 * NDT, 6>();
       pa_prev[0] = pa_new[0];
       pa_prev[1] = pa_new[1];
       s_cur = s_next;
@@ -904,9 +1006,9 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
 // ---------------------------------------------------------------------------
 int tokens_per_block16(int group) { return NWAVE16 * 32 / group; }
 
-template <typename T, int D, int G>
+template <typename T, typename KV, int D, int G>
 int launch16(PrefillParams p, int max_e, hipStream_t stream) {
-  using Geo = G16<D>;
+  using Geo = G16<D, (int)sizeof(KV)>;
   constexpr int BQ = Geo::ROWS / G;
   p.nqb = (max_e + BQ - 1) / BQ;
   const int64_t items = (int64_t)p.hkv * p.num_reqs * p.splits * p.nqb;
@@ -923,14 +1025,14 @@ int launch16(PrefillParams p, int max_e, hipStream_t stream) {
   const int grid = (int)items;
   static bool attr_set = false;  // per process; the attribute is per function
   if (Geo::LDS_BYTES > 65536 && !attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill16_kernel<T, D, G>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill16_kernel<T, KV, D, G>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, Geo::LDS_BYTES) != hipSuccess) {
       set_error("msgl_prefill_ragged: cannot raise the LDS limit to %d bytes", Geo::LDS_BYTES);
       return MSGL_ERR_HIP;
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((prefill16_kernel<T, D, G>), dim3(grid), dim3(THREADS16), Geo::LDS_BYTES, stream, p);
+  hipLaunchKernelGGL((prefill16_kernel<T, KV, D, G>), dim3(grid), dim3(THREADS16), Geo::LDS_BYTES, stream, p);
   MSGL_CHECK_LAUNCH("msgl_prefill_ragged");
   if (p.splits > 1) {
     constexpr int HPB = 256 / (D / 4);
@@ -951,36 +1053,36 @@ int launch32(const PrefillParams& p, int max_e, hipStream_t stream) {
   return MSGL_OK;
 }
 
-template <typename T, int D, int G>
+template <typename T, typename KV, int D, int G>
 int launch_prefill(const PrefillParams& p, int max_e, hipStream_t s) {
   if constexpr (sizeof(T) == 4) {
     if (p.mode == kPlanOnly) return MSGL_OK;  // the fp32 path has no work list
     return launch32<D, G>(p, max_e, s);
   } else {
-    return launch16<T, D, G>(p, max_e, s);
+    return launch16<T, KV, D, G>(p, max_e, s);
   }
 }
 
-template <typename T, int D>
+template <typename T, typename KV, int D>
 int prefill_group(const PrefillParams& p, int max_e, int group, hipStream_t s) {
   switch (group) {
-    case 1: return launch_prefill<T, D, 1>(p, max_e, s);
-    case 2: return launch_prefill<T, D, 2>(p, max_e, s);
-    case 4: return launch_prefill<T, D, 4>(p, max_e, s);
-    case 8: return launch_prefill<T, D, 8>(p, max_e, s);
-    case 16: return launch_prefill<T, D, 16>(p, max_e, s);
+    case 1: return launch_prefill<T, KV, D, 1>(p, max_e, s);
+    case 2: return launch_prefill<T, KV, D, 2>(p, max_e, s);
+    case 4: return launch_prefill<T, KV, D, 4>(p, max_e, s);
+    case 8: return launch_prefill<T, KV, D, 8>(p, max_e, s);
+    case 16: return launch_prefill<T, KV, D, 16>(p, max_e, s);
     default:
       set_error("msgl_prefill_ragged: Hq/Hkv = %d not built (1, 2, 4, 8, 16)", group);
       return MSGL_ERR_UNSUPPORTED;
   }
 }
 
-template <typename T>
+template <typename T, typename KV = T>
 int prefill_dim(const PrefillParams& p, int max_e, int head_dim, int group, hipStream_t s) {
   switch (head_dim) {
-    case 64: return prefill_group<T, 64>(p, max_e, group, s);
-    case 128: return prefill_group<T, 128>(p, max_e, group, s);
-    case 256: return prefill_group<T, 256>(p, max_e, group, s);
+    case 64: return prefill_group<T, KV, 64>(p, max_e, group, s);
+    case 128: return prefill_group<T, KV, 128>(p, max_e, group, s);
+    case 256: return prefill_group<T, KV, 256>(p, max_e, group, s);
     default:
       set_error("msgl_prefill_ragged: head_dim %d not built (64, 128, 256)", head_dim);
       return MSGL_ERR_UNSUPPORTED;
@@ -1040,7 +1142,7 @@ extern "C" int64_t msgl_prefill_workspace_size(int32_t num_reqs, int32_t num_tok
 
 namespace {
 int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, const void* v_pool,
-                 const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                 const float* kv_scale, const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
                  const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
                  int32_t max_seq_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                  int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
@@ -1062,6 +1164,7 @@ int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, co
     MSGL_CHECK_ARG(q && k_pool && v_pool && kv_indices && out, "%s: null pointer", fn);
     MSGL_CHECK_ARG(((uintptr_t)q | (uintptr_t)k_pool | (uintptr_t)v_pool | (uintptr_t)out) % 16 == 0,
                    "%s: q, pools and out must be 16-byte aligned", fn);
+    MSGL_CHECK_ARG((uintptr_t)kv_scale % 8 == 0, "%s: kv_scale must be 8-byte aligned", fn);
   }
   if (dtype_size(dtype) == 0) {
     set_error("%s: unknown dtype %d", fn, dtype);
@@ -1071,6 +1174,7 @@ int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, co
   p.q = q;
   p.k_pool = k_pool;
   p.v_pool = v_pool;
+  p.kv_scale = kv_scale;
   p.q_indptr = q_indptr;
   p.kv_indptr = kv_indptr;
   p.kv_indices = kv_indices;
@@ -1118,6 +1222,14 @@ int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, co
   }
   const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
+  if (kv_scale != nullptr) {  // fp8 e4m3 pools with per-(slot, kv head) scales
+    switch (dtype) {
+      case MSGL_BF16: return prefill_dim<bf16_t, fp8e4m3>(p, max_extend_len, head_dim, group, s);
+      case MSGL_F16: return prefill_dim<f16_t, fp8e4m3>(p, max_extend_len, head_dim, group, s);
+    }
+    set_error("%s: fp8 pools take bf16 or fp16 queries (dtype %d)", fn, dtype);
+    return MSGL_ERR_UNSUPPORTED;
+  }
   switch (dtype) {
     case MSGL_F32: return prefill_dim<float>(p, max_extend_len, head_dim, group, s);
     case MSGL_BF16: return prefill_dim<bf16_t>(p, max_extend_len, head_dim, group, s);
@@ -1133,7 +1245,8 @@ extern "C" int msgl_prefill_ragged(const void* q, const void* k_pool, const void
                                    int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
                                    int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                                    void* workspace, int64_t workspace_bytes, void* stream) {
-  return prefill_impl("msgl_prefill_ragged", msgl::kPlanAndRun, q, k_pool, v_pool, q_indptr, kv_indptr, kv_indices,
+  return prefill_impl("msgl_prefill_ragged", msgl::kPlanAndRun, q, k_pool, v_pool, nullptr, q_indptr, kv_indptr,
+                      kv_indices,
                       seq_lens, num_reqs, num_tokens, max_extend_len, max_seq_len, num_qo_heads, num_kv_heads,
                       head_dim, page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes,
                       stream);
@@ -1147,7 +1260,8 @@ extern "C" int msgl_prefill_ragged_planned(const void* q, const void* k_pool, co
                                            int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
                                            int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
                                            void* stream) {
-  return prefill_impl("msgl_prefill_ragged_planned", msgl::kRunPlanned, q, k_pool, v_pool, q_indptr, kv_indptr,
+  return prefill_impl("msgl_prefill_ragged_planned", msgl::kRunPlanned, q, k_pool, v_pool, nullptr, q_indptr,
+                      kv_indptr,
                       kv_indices, seq_lens, num_reqs, num_tokens, max_extend_len, max_seq_len, num_qo_heads,
                       num_kv_heads, head_dim, page_size, num_slots, dtype, scale, max_splits, out, workspace,
                       workspace_bytes, stream);
@@ -1157,7 +1271,41 @@ extern "C" int msgl_prefill_plan(const int32_t* q_indptr, const int32_t* kv_indp
                                  int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
                                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
                                  int32_t max_splits, void* workspace, int64_t workspace_bytes, void* stream) {
-  return prefill_impl("msgl_prefill_plan", msgl::kPlanOnly, nullptr, nullptr, nullptr, q_indptr, kv_indptr, nullptr,
+  return prefill_impl("msgl_prefill_plan", msgl::kPlanOnly, nullptr, nullptr, nullptr, nullptr, q_indptr, kv_indptr,
+                      nullptr,
                       seq_lens, num_reqs, num_tokens, max_extend_len, max_seq_len, num_qo_heads, num_kv_heads,
                       head_dim, 1, 1, dtype, 1.f, max_splits, nullptr, workspace, workspace_bytes, stream);
+}
+
+extern "C" int msgl_prefill_ragged_fp8(const void* q, const void* k_pool, const void* v_pool, const float* kv_scale,
+                                       const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                                       const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens,
+                                       int32_t max_extend_len, int32_t max_seq_len, int32_t num_qo_heads,
+                                       int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                                       int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(kv_scale != nullptr, "msgl_prefill_ragged_fp8: null kv_scale");
+  return prefill_impl("msgl_prefill_ragged_fp8", kPlanAndRun, q, k_pool, v_pool, kv_scale, q_indptr, kv_indptr,
+                      kv_indices, seq_lens, num_reqs, num_tokens, max_extend_len, max_seq_len, num_qo_heads,
+                      num_kv_heads, head_dim, page_size, num_slots, dtype, scale, max_splits, out, workspace,
+                      workspace_bytes, stream);
+}
+
+extern "C" int msgl_prefill_ragged_fp8_planned(const void* q, const void* k_pool, const void* v_pool,
+                                               const float* kv_scale, const int32_t* q_indptr,
+                                               const int32_t* kv_indptr, const int32_t* kv_indices,
+                                               const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens,
+                                               int32_t max_extend_len, int32_t max_seq_len, int32_t num_qo_heads,
+                                               int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                               int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                                               void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(kv_scale != nullptr, "msgl_prefill_ragged_fp8_planned: null kv_scale");
+  return prefill_impl("msgl_prefill_ragged_fp8_planned", kRunPlanned, q, k_pool, v_pool, kv_scale, q_indptr,
+                      kv_indptr, kv_indices, seq_lens, num_reqs, num_tokens, max_extend_len, max_seq_len,
+                      num_qo_heads, num_kv_heads, head_dim, page_size, num_slots, dtype, scale, max_splits, out,
+                      workspace, workspace_bytes, stream);
 }

@@ -113,6 +113,12 @@ SIGNATURES["msgl_paged_decode_fp8"] = (
 )
 SIGNATURES["msgl_paged_decode_fp8_planned"] = SIGNATURES["msgl_paged_decode_fp8"]
 SIGNATURES["msgl_prefill_ragged_planned"] = SIGNATURES["msgl_prefill_ragged"]
+SIGNATURES["msgl_prefill_ragged_fp8"] = (
+    ctypes.c_int,
+    [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32,
+     _c_i64, _c_i32, _c_f, _c_i32, _c_p, _c_p, _c_i64, _c_p],
+)
+SIGNATURES["msgl_prefill_ragged_fp8_planned"] = SIGNATURES["msgl_prefill_ragged_fp8"]
 SIGNATURES["msgl_prefill_plan"] = (
     ctypes.c_int,
     [_c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_i64, _c_p],

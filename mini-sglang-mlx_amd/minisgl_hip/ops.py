@@ -280,6 +280,7 @@ def prefill_ragged_attention(
     out: Optional[torch.Tensor] = None,
     workspace: Optional[torch.Tensor] = None,
     planned: bool = False,
+    kv_scale: Optional[torch.Tensor] = None,
 ) -> torch.Tensor:
     """Ragged prefill over cached prefixes; counterpart of attention/base.py:85-105.
 
@@ -291,6 +292,8 @@ def prefill_ragged_attention(
     split (its default and the chunk length). ``workspace`` (from ``prefill_workspace``) is allocated per
     call when the split needs one and none large enough is given. With ``planned`` the workspace
     already holds the work list ``prefill_plan`` built for these indices and sizes.
+    fp8 pools (``torch.float8_e4m3fn``, written by ``store_kv_fp8``) take ``kv_scale``
+    (float32 [N, Hkv, 2]) and bf16/fp16 queries.
     """
     if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
         raise ValueError("q must be [T, Hq, D] and pools [N, Hkv, D]")
@@ -298,7 +301,16 @@ def prefill_ragged_attention(
     n_slots, hkv, dk = k_pool.shape
     if dk != d or hq % hkv != 0:
         raise ValueError(f"head_dim mismatch or Hq ({hq}) not a multiple of Hkv ({hkv})")
-    if len({q.dtype, k_pool.dtype, v_pool.dtype}) != 1:
+    fp8 = k_pool.dtype == torch.float8_e4m3fn
+    if fp8:
+        if v_pool.dtype != k_pool.dtype or kv_scale is None:
+            raise ValueError("fp8 pools need both pools fp8 and kv_scale")
+        if q.dtype not in (torch.bfloat16, torch.float16):
+            raise ValueError("fp8 pools take bf16 or fp16 queries")
+        if kv_scale.dtype != torch.float32 or kv_scale.shape != (n_slots, hkv, 2):
+            raise ValueError("kv_scale must be float32 [N, Hkv, 2]")
+        _check_device("kv_scale", kv_scale, q.device)
+    elif len({q.dtype, k_pool.dtype, v_pool.dtype}) != 1:
         raise ValueError("q and pools must share one dtype")
     if page_size > 1 and seq_lens is None:
         raise ValueError("page_size > 1 needs seq_lens")
@@ -331,9 +343,14 @@ def prefill_ragged_attention(
             raise ValueError("planned prefill needs the workspace its plan was built in")
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
-    fn = lib.msgl_prefill_ragged_planned if planned else lib.msgl_prefill_ragged
+    if fp8:
+        fn = lib.msgl_prefill_ragged_fp8_planned if planned else lib.msgl_prefill_ragged_fp8
+        pools = (_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool), _lib.ptr(kv_scale))
+    else:
+        fn = lib.msgl_prefill_ragged_planned if planned else lib.msgl_prefill_ragged
+        pools = (_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool))
     status = fn(
-        _lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool),
+        *pools,
         _lib.ptr(q_indptr), _lib.ptr(kv_indptr), _lib.ptr(kv_indices), _lib.ptr(seq_lens),
         num_reqs, t, int(max_extend_len), int(max_seq_len), hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
         int(max_splits), _lib.ptr(out), _lib.ptr(workspace), ws_bytes, _lib.current_stream(dev),

@@ -20,14 +20,14 @@ def _codes(t):
     return t.view(torch.uint8).cpu().numpy()
 
 
-def _fp8_pools(n, hkv, d, seed, device, src_dtype=torch.bfloat16, spread=True):
+def _fp8_pools(n, hkv, d, seed, device, src_dtype=torch.bfloat16, spread=2.0):
     """Quantise random rows into every slot with the HIP store; returns (kp, vp, kv_scale, k_src, v_src)."""
     g = torch.Generator(device=device).manual_seed(seed)
     k = torch.randn((n, hkv, d), generator=g, device=device, dtype=torch.float32)
     v = torch.randn((n, hkv, d), generator=g, device=device, dtype=torch.float32)
-    if spread:  # rows of very different magnitudes, so the per-row scales matter
-        k *= torch.exp(torch.randn((n, hkv, 1), generator=g, device=device) * 2)
-        v *= torch.exp(torch.randn((n, hkv, 1), generator=g, device=device) * 2)
+    if spread:  # rows of very different magnitudes (log-normal, sigma = spread), so the per-row scales matter
+        k *= torch.exp(torch.randn((n, hkv, 1), generator=g, device=device) * spread)
+        v *= torch.exp(torch.randn((n, hkv, 1), generator=g, device=device) * spread)
     k, v = k.to(src_dtype), v.to(src_dtype)
     kp = torch.empty((n, hkv, d), dtype=FP8, device=device)
     vp = torch.empty_like(kp)
@@ -140,7 +140,7 @@ def test_fp8_decode_headline_batch(cuda_device):
     """The headline decode shape (batch 128, L ~ U[200, 2048], 262144-slot pool) over an fp8 pool:
     sampled requests vs the oracle, and the quantisation error against the unquantised decode."""
     c = workloads.decode_case(128, 200, 2048, 262144, 1, seed=0)
-    kp, vp, sc, k_src, v_src = _fp8_pools(262144, 8, 128, 400, cuda_device, spread=False)
+    kp, vp, sc, k_src, v_src = _fp8_pools(262144, 8, 128, 400, cuda_device, spread=0)
     q = randn((128, 16, 128), 401, torch.bfloat16).to(cuda_device)
     ip, ix = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
     print("case fp8 headline", flush=True)
@@ -158,3 +158,81 @@ def test_fp8_decode_headline_batch(cuda_device):
     rel = ((out.float() - exact.float()).norm() / exact.float().norm()).item()
     print(f"fp8 vs bf16 decode relative error {rel:.4f}", flush=True)
     assert rel < 0.05
+
+
+def _fp8_prefill(case, hq, hkv, d, dt, device, seed, splits=None, page_size=1, planned=False):
+    """Quantise a random pool (prefix rows) and this step's rows into fp8, then run
+    the ragged prefill over it; returns (q, kp, vp, kv_scale, out)."""
+    n = case.num_slots
+    # P enters the matrix core in 16 bits, so the output error scales with max |V|: moderate row spread
+    kp, vp, sc, _, _ = _fp8_pools(n, hkv, d, seed, device, spread=0.5)
+    q = randn((case.num_tokens, hq, d), seed + 2, dt).to(device)
+    knew = randn((case.num_tokens, hkv, d), seed + 3, dt).to(device)
+    vnew = randn((case.num_tokens, hkv, d), seed + 4, dt).to(device)
+    ops.store_kv_fp8(knew, vnew, i32(case.out_loc, device), kp, vp, sc)
+    if page_size == 1:
+        kv_indptr, kv_indices, seq = case.kv_indptr, case.kv_indices, None
+    else:
+        pages = [case.page_table[i, : int(L)][::page_size] // page_size for i, L in enumerate(case.seq_lens)]
+        kv_indptr = np.concatenate([[0], np.cumsum([len(x) for x in pages])]).astype(np.int32)
+        kv_indices = np.concatenate(pages).astype(np.int32)
+        seq = case.seq_lens
+    args = (q, kp, vp, i32(case.q_indptr, device), i32(kv_indptr, device), i32(kv_indices, device),
+            None if seq is None else i32(seq, device), d**-0.5)
+    maxe, maxs = int(case.extend_lens.max()), int(case.seq_lens.max())
+    if splits is None:
+        splits = ops.prefill_default_splits(len(case.seq_lens), hq, hkv, d, maxe, maxs)
+    ws = ops.prefill_workspace(len(case.seq_lens), case.num_tokens, maxe, hq, hkv, d, splits, device)
+    if planned:
+        ops.prefill_plan(args[3], args[4], args[6], num_tokens=case.num_tokens, max_extend_len=maxe,
+                         max_seq_len=maxs, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, dtype=dt,
+                         max_splits=splits, workspace=ws)
+    out = ops.prefill_ragged_attention(*args, max_extend_len=maxe, max_seq_len=maxs, page_size=page_size,
+                                       max_splits=splits, workspace=ws, planned=planned, kv_scale=sc)
+    torch.cuda.synchronize()
+    return q, kp, vp, sc, out
+
+
+def _fp8_prefill_oracle(case, q, kp, vp, sc, d):
+    kvi = [case.kv_indices[case.kv_indptr[i]: case.kv_indptr[i + 1]] for i in range(len(case.seq_lens))]
+    return oracle.forward_prefill(to_np64(q), None, None, _deq(kp, sc, 0), _deq(vp, sc, 1),
+                                  case.q_indptr.tolist(), kvi, d**-0.5)
+
+
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256)])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_fp8_prefill_grid(cuda_device, dt, hq, hkv, d, splits):
+    """Prefix P in {0,1,17,300,0}, extend E in {1,2,64,100,37} over fp8 pools (the
+    step's rows quantised by the fp8 store first)."""
+    dtype = DTYPES[dt]
+    case = workloads.prefill_case_from_lens([0, 1, 17, 300, 0], [1, 2, 64, 100, 37], num_slots=2048, seed=3)
+    print(f"case fp8 prefill grid {hq}/{hkv}/{d} {dt} splits={splits}", flush=True)
+    q, kp, vp, sc, out = _fp8_prefill(case, hq, hkv, d, dtype, cuda_device, 10, splits=splits)
+    assert_close(out, _fp8_prefill_oracle(case, q, kp, vp, sc, d), dtype, f"fp8 prefill {hq}/{hkv}/{d} {dt}")
+
+
+def test_fp8_prefill_page16_and_planned(cuda_device):
+    case = workloads.prefill_case_from_lens([0, 15, 16, 40, 333, 1500], [5, 1, 33, 100, 64, 300], num_slots=8192,
+                                            page_size=16, seed=4)
+    print("case fp8 prefill page16", flush=True)
+    q, kp, vp, sc, out = _fp8_prefill(case, 32, 8, 128, torch.bfloat16, cuda_device, 20, page_size=16)
+    assert_close(out, _fp8_prefill_oracle(case, q, kp, vp, sc, 128), torch.bfloat16, "fp8 prefill page16")
+    _, _, _, _, out2 = _fp8_prefill(case, 32, 8, 128, torch.bfloat16, cuda_device, 20, page_size=16, planned=True)
+    assert torch.equal(out, out2), "planned fp8 prefill differs"
+
+
+def test_fp8_prefill_workload(cuda_device):
+    """The 16-request prefill workload over an fp8 pool: sampled requests vs the oracle."""
+    case = workloads.prefill_case(16, 4096, 64, 512, 2048, num_slots=1 << 17, seed=0)
+    print("case fp8 prefill workload", flush=True)
+    q, kp, vp, sc, out = _fp8_prefill(case, 16, 8, 128, torch.bfloat16, cuda_device, 30)
+    for i in (0, 7, 15):
+        s, e = int(case.q_indptr[i]), int(case.q_indptr[i + 1])
+        slots = torch.from_numpy(case.kv_indices[case.kv_indptr[i]: case.kv_indptr[i + 1]].astype(np.int64))
+        slots = slots.to(cuda_device)
+        kb = oracle.dequantize_fp8(_codes(kp[slots]), sc[slots][..., 0].cpu().numpy())
+        vb = oracle.dequantize_fp8(_codes(vp[slots]), sc[slots][..., 1].cpu().numpy())
+        ref = oracle.forward_prefill(to_np64(q[s:e]), None, None, kb, vb, [0, e - s], [np.arange(len(slots))],
+                                     128**-0.5)
+        assert_close(out[s:e], ref, torch.bfloat16, f"fp8 prefill workload request {i}")
