@@ -26,6 +26,7 @@ Other workloads (one JSON line each, same fields):
             prefixes 0 and 8192, indices built on the GPU from the page table
   decode_fp8  the default decode workload over fp8 e4m3 pools with one scale
             per slot and kv head (quantising store + fp8 decode per layer)
+  prefill_fp8 the prefill workload over fp8 e4m3 pools
   rope      rotate-half RoPE of q and k fused with the KV store over the
             prefill workload's 2040 packed tokens (Qwen3-0.6B heads), 28 layers
 """
@@ -54,7 +55,8 @@ TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_b128_ctx2k_traffic.txt"
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "decode_fp8", "prefill", "mixed", "rope", "ceilings"])
+    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "decode_fp8", "prefill", "prefill_fp8", "mixed", "rope",
+                                                    "ceilings"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
@@ -143,7 +145,8 @@ def main():
         del src, dst
     if args.workload != "decode":
         line = {"decode8b": bench_decode8b, "prefill": bench_prefill, "mixed": bench_mixed,
-                "rope": bench_rope, "decode_fp8": bench_decode_fp8, "ceilings": bench_ceilings}[args.workload](args, dev)
+                "rope": bench_rope, "decode_fp8": bench_decode_fp8, "ceilings": bench_ceilings,
+                "prefill_fp8": lambda a, d: bench_prefill(a, d, fp8=True)}[args.workload](args, dev)
         print(json.dumps(line), flush=True)
         return
     bench_decode(args, dev)
@@ -452,8 +455,9 @@ def bench_decode8b(args, dev):
 MFMA_PEAK_TFLOPS = 2500.0
 
 
-def bench_prefill(args, dev):
-    """Ragged prefill, 16 requests over cached prefixes, Qwen3-0.6B heads; 28 layers' pools in rotation."""
+def bench_prefill(args, dev, fp8=False):
+    """Ragged prefill, 16 requests over cached prefixes, Qwen3-0.6B heads; 28 layers' pools in rotation
+    (bf16 pools, or fp8 pools with per-slot, per-kv-head scales)."""
     import torch
 
     from minisgl_hip import ops, workloads
@@ -461,9 +465,26 @@ def bench_prefill(args, dev):
     pool = 1 << 17
     case = workloads.prefill_case(16, 4096, 64, 512, 2048, num_slots=pool, seed=0)
     flops, nbytes = workloads.prefill_flops_bytes(case.prefix_lens, case.extend_lens, HQ, HKV, D, 2)
+    if fp8:  # K/V rows of D one-byte codes + 8 bytes of scales instead of 2 D bytes
+        kv_rows = int((case.prefix_lens + case.extend_lens).sum())
+        nbytes -= kv_rows * HKV * (2 * D * 2 - (D + 4) * 2)
     gen = torch.Generator(device=dev).manual_seed(0)
-    kps = [torch.randn((pool, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
-    vps = [torch.randn((pool, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(LAYERS)]
+    kps, vps, scs = [], [], []
+    all_slots = torch.arange(pool, dtype=torch.int32, device=dev)
+    for _ in range(LAYERS):
+        kb = torch.randn((pool, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        vb = torch.randn((pool, HKV, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        if fp8:
+            kq = torch.empty((pool, HKV, D), dtype=torch.float8_e4m3fn, device=dev)
+            vq = torch.empty_like(kq)
+            sc = torch.empty((pool, HKV, 2), dtype=torch.float32, device=dev)
+            ops.store_kv_fp8(kb, vb, all_slots, kq, vq, sc)
+            kb, vb = kq, vq
+            scs.append(sc)
+        else:
+            scs.append(None)
+        kps.append(kb)
+        vps.append(vb)
     t = case.num_tokens
     q = torch.randn((t, HQ, D), generator=gen, device=dev, dtype=torch.bfloat16)
     out = torch.empty_like(q)
@@ -479,27 +500,34 @@ def bench_prefill(args, dev):
             ops.prefill_plan(qi, ki, None, num_tokens=t, max_extend_len=maxe, max_seq_len=maxs, num_qo_heads=HQ,
                              num_kv_heads=HKV, head_dim=D, dtype=torch.bfloat16, max_splits=splits, workspace=ws)
         ops.prefill_ragged_attention(q, kps[layer], vps[layer], qi, ki, kx, None, D**-0.5, max_extend_len=maxe,
-                                     max_seq_len=maxs, max_splits=splits, out=out, workspace=ws, planned=True)
+                                     max_seq_len=maxs, max_splits=splits, out=out, workspace=ws, planned=True,
+                                     kv_scale=scs[layer])
 
     step = _b2b_step_time(args, run_layer, LAYERS)
     sec = step / LAYERS  # one layer: attention + split-K merge (+ 1/28 of the plan)
     tflops = flops / sec / 1e12
     gbs = nbytes / sec / 1e9
-    return _line(
-        args, "ragged-prefill attention µs/layer, 16 requests over cached prefixes, Qwen3-0.6B heads",
+    line = _line(
+        args, "ragged-prefill attention µs/layer, 16 requests over cached prefixes, Qwen3-0.6B heads"
+        + (", fp8 KV cache" if fp8 else ""),
         sec * 1e6, "us", step * 1e3,
         "ragged chunked prefill, Qwen3-0.6B attention (16 q / 8 kv heads, head_dim 128); 16 requests, prefix "
         "U[0,4096], extend U[64,512] rescaled to <= 2048 packed tokens (seed 0), page_size 1, 131072-slot "
-        "bf16 pools; one step = one work-list plan + the 28 layers back to back (median of steps), each layer "
+        + ("fp8 e4m3 pools (one fp32 K and V scale per slot and kv head)" if fp8 else "bf16 pools")
+        + "; one step = one work-list plan + the 28 layers back to back (median of steps), each layer "
         "attention + split-K merge; bottom-right causal",
         {"requests": 16, "packed_tokens": t, "sum_prefix": int(case.prefix_lens.sum()), "max_splits": splits,
          "flops_per_step": flops, "bytes_per_step": nbytes, "tflops": round(tflops, 2),
          "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4)},
         {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(gbs / HBM_PEAK_GBS, 4),
-         "traffic": read_traffic(ROOT / "profiles" / "prefill_ragged_16req_traffic.txt")},
+         "traffic": read_traffic(ROOT / "profiles" / ("prefill_ragged_16req_fp8_traffic.txt" if fp8
+                                                      else "prefill_ragged_16req_traffic.txt"))},
         higher=False,
     )
+    if fp8:
+        line["dtype"] = "fp8 e4m3 KV, bf16 q/out, fp32 accumulation"
+    return line
 
 
 def bench_rope(args, dev):

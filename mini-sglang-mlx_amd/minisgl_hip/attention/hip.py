@@ -69,13 +69,19 @@ class HipAttnBackend(BaseAttnBackend):
     def __init__(self, config, kv_cache, page_table: np.ndarray, fuse_decode_store: bool = True) -> None:
         super().__init__(config, kv_cache, page_table)
         self.device = kv_cache.k[0].device
-        self.fuse_decode_store = fuse_decode_store and hasattr(kv_cache, "take_pending")
+        # an fp8 pool quantises in its own store: no fused store in the decode launch
+        self.fuse_decode_store = (fuse_decode_store and hasattr(kv_cache, "take_pending")
+                                  and not getattr(kv_cache, "quantized", False))
 
     def prepare_metadata(self, batch: "Batch") -> None:
         if self.fuse_decode_store:
             self.kv_cache.flush()
             self.kv_cache.defer_stores = batch.is_decode
         super().prepare_metadata(batch)
+
+    def _kv_scale(self, layer_id: int) -> Optional[torch.Tensor]:
+        """fp8 pools: the layer's (K, V) scales; None for unquantised pools."""
+        return self.kv_cache.kv_scale[layer_id] if getattr(self.kv_cache, "quantized", False) else None
 
     # ------------------------------------------------------------------ decode
 
@@ -122,6 +128,7 @@ class HipAttnBackend(BaseAttnBackend):
             workspace=ws,
             new_kv=pending,
             planned=True,
+            kv_scale=self._kv_scale(layer_id),
         )
 
     # ------------------------------------------------------------------ prefill
@@ -185,4 +192,5 @@ class HipAttnBackend(BaseAttnBackend):
             max_splits=d.max_splits,
             workspace=d.workspace,
             planned=d.workspace is not None,
+            kv_scale=self._kv_scale(layer_id),
         )

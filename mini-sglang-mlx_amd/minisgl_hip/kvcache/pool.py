@@ -12,6 +12,11 @@ steps), ``store_kv`` only records the rows; the backend then performs the
 store inside its decode launch (``take_pending``). Any other read of that
 layer's pool (``k_cache``/``v_cache``) first performs the recorded store, so
 every reader still observes the pool exactly as after an eager store.
+
+fp8 pools (``kv_dtype=torch.float8_e4m3fn``, the extension docs/09-exercises.md:81-82
+describes): ``k``/``v`` hold e4m3 codes and ``kv_scale[layer]`` [num_tokens,
+num_kv_heads, 2] the K and V scale of each slot and head; ``store_kv``
+quantises (never deferred), ``dtype`` stays the model's (q/k/v) type.
 """
 
 from __future__ import annotations
@@ -34,10 +39,19 @@ class MHAKVCache:
         head_dim: int,
         dtype: torch.dtype,
         device: torch.device | str = "cuda",
+        kv_dtype: Optional[torch.dtype] = None,
     ) -> None:
         shape = (num_tokens, num_kv_heads, head_dim)
-        self.k: List[torch.Tensor] = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(num_layers)]
-        self.v: List[torch.Tensor] = [torch.zeros(shape, dtype=dtype, device=device) for _ in range(num_layers)]
+        kv_dtype = dtype if kv_dtype is None else kv_dtype
+        if kv_dtype not in (dtype, torch.float8_e4m3fn):
+            raise ValueError("kv_dtype must be the model dtype or torch.float8_e4m3fn")
+        self.quantized = kv_dtype == torch.float8_e4m3fn
+        self.k: List[torch.Tensor] = [torch.zeros(shape, dtype=kv_dtype, device=device) for _ in range(num_layers)]
+        self.v: List[torch.Tensor] = [torch.zeros(shape, dtype=kv_dtype, device=device) for _ in range(num_layers)]
+        self.kv_scale: List[Optional[torch.Tensor]] = [
+            torch.zeros((num_tokens, num_kv_heads, 2), dtype=torch.float32, device=device) if self.quantized else None
+            for _ in range(num_layers)
+        ]
         self.num_layers = num_layers
         self.num_tokens = num_tokens
         self.num_kv_heads = num_kv_heads
@@ -56,7 +70,9 @@ class MHAKVCache:
 
     def store_kv(self, k: torch.Tensor, v: torch.Tensor, out_loc: torch.Tensor, layer_id: int) -> None:
         """kvcache/pool.py:47-50: write this step's k/v ([T, Hkv, D]) to slots out_loc ([T])."""
-        if self.defer_stores:
+        if self.quantized:
+            ops.store_kv_fp8(k, v, out_loc, self.k[layer_id], self.v[layer_id], self.kv_scale[layer_id])
+        elif self.defer_stores:
             self.flush(layer_id)
             self._pending[layer_id] = (k, v, out_loc)
         else:
@@ -70,6 +86,11 @@ class MHAKVCache:
         ``rotary`` carries ``inv_freq`` and ``dims`` (a ``layers.RotaryEmbedding``).
         The store happens now, whatever ``defer_stores`` says."""
         self.flush(layer_id)
+        if self.quantized:  # rotate, then the quantising store
+            q_rot = ops.rope(q, positions, rotary.inv_freq, rotary.dims, out=q_out)
+            k_rot = ops.rope(k, positions, rotary.inv_freq, rotary.dims, out=k_out)
+            self.store_kv(k_rot, v, out_loc, layer_id)
+            return q_rot
         return ops.rope_store_kv(q, k, v, positions, out_loc, self.k[layer_id], self.v[layer_id], rotary.inv_freq,
                                  rotary.dims, q_out=q_out, k_out=k_out)
 
@@ -89,4 +110,5 @@ class MHAKVCache:
 
     @property
     def nbytes(self) -> int:
-        return 2 * self.num_layers * self.k[0].numel() * self.k[0].element_size()
+        scales = self.kv_scale[0].numel() * 4 if self.quantized else 0
+        return self.num_layers * (2 * self.k[0].numel() * self.k[0].element_size() + scales)

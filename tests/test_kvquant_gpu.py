@@ -236,3 +236,74 @@ def test_fp8_prefill_workload(cuda_device):
         ref = oracle.forward_prefill(to_np64(q[s:e]), None, None, kb, vb, [0, e - s], [np.arange(len(slots))],
                                      128**-0.5)
         assert_close(out[s:e], ref, torch.bfloat16, f"fp8 prefill workload request {i}")
+
+
+def test_backend_with_fp8_cache(cuda_device):
+    """The attention layer and hip backend over an fp8 KV cache (layers.py:103-111 order:
+    rotate, quantising store, attention): a chunked prefill with a cached prefix,
+    then a decode step, vs the oracle over the dequantised pool."""
+    from minisgl_hip.attention import create_attention_backend
+    from minisgl_hip.core import Batch, Context, ModelConfig, Req, RotaryConfig, set_global_ctx
+    from minisgl_hip.kvcache import MHAKVCache
+    from minisgl_hip.layers import AttentionLayer
+
+    dt = torch.bfloat16
+    cfg = ModelConfig(num_qo_heads=16, num_kv_heads=8, head_dim=128, num_layers=2)
+    kv = MHAKVCache(2, 8192, 8, 128, dt, cuda_device, kv_dtype=FP8)
+    assert kv.quantized and kv.k[0].dtype == FP8 and kv.kv_scale[0].shape == (8192, 8, 2)
+    table = np.zeros((8, 1024), dtype=np.int32)
+    backend = create_attention_backend("hip", cfg, kv, table)
+    ctx = Context(page_size=1)
+    ctx.page_table, ctx.kv_cache, ctx.attn_backend = table, kv, backend
+    layers = [AttentionLayer(i, 16, 8, 128, RotaryConfig(head_dim=128, rotary_dim=128, base=1e6), cuda_device)
+              for i in range(2)]
+    set_global_ctx(ctx)
+    try:
+        free = np.random.default_rng(30).permutation(8192).astype(np.int32)
+        reqs = [Req(input_ids=np.zeros(50, np.int32), table_idx=0, cached_len=20),
+                Req(input_ids=np.zeros(33, np.int32), table_idx=1, cached_len=0)]
+        free = oracle.allocate_paged(table, free, [0, 1], [0, 0], [50, 33], 1)
+        all_slots = torch.arange(8192, dtype=torch.int32, device=cuda_device)
+        for layer in range(2):  # the cached prefix: quantised rows in every slot
+            kv.store_kv(randn((8192, 8, 128), 31 + layer, dt).to(cuda_device),
+                        randn((8192, 8, 128), 33 + layer, dt).to(cuda_device), all_slots, layer)
+        inv = oracle.rope_inv_freq(128, 1e6)
+        for phase in ("prefill", "decode"):
+            batch = Batch(reqs=reqs, phase=phase)
+            if phase == "decode":
+                free = oracle.allocate_paged(table, free, [0, 1], [r.cached_len for r in reqs],
+                                             [r.device_len for r in reqs], 1)
+            rows = [r.table_idx for r in reqs]
+            cached, dlen = [r.cached_len for r in reqs], [r.device_len for r in reqs]
+            pos, out_loc = oracle.prepare_batch_indices(table, rows, cached, dlen)
+            batch.positions, batch.out_loc = i32(pos, cuda_device), i32(out_loc, cuda_device)
+            backend.prepare_metadata(batch)
+            with ctx.forward_batch(batch):
+                for layer in range(2):
+                    t = len(pos)
+                    q = randn((t, 16, 128), 40 + layer, dt).to(cuda_device)
+                    k = randn((t, 8, 128), 50 + layer, dt).to(cuda_device)
+                    v = randn((t, 8, 128), 60 + layer, dt).to(cuda_device)
+                    print(f"case fp8 backend {phase} layer={layer}", flush=True)
+                    o = layers[layer](q, k, v)
+                    torch.cuda.synchronize()
+                    kp, vp = _deq(kv.k[layer], kv.kv_scale[layer], 0), _deq(kv.v[layer], kv.kv_scale[layer], 1)
+                    # the step's rows were quantised from the rotated k and the raw v
+                    kc, _ = oracle.quantize_fp8(oracle.rope(to_np64(k), pos, 128, inv).astype(np.float32))
+                    vc, _ = oracle.quantize_fp8(to_np64(v).astype(np.float32))
+                    assert (np.abs(oracle.e4m3_decode(_codes(kv.k[layer])[out_loc]).astype(np.float64)
+                                   - oracle.e4m3_decode(kc)) <= np.abs(oracle.e4m3_decode(kc)) / 8 + 1e-6).all()
+                    np.testing.assert_array_equal(_codes(kv.v[layer])[out_loc], vc)
+                    q_rot = oracle.rope(to_np64(q), pos, 128, inv)
+                    if phase == "prefill":
+                        offs = np.concatenate([[0], np.cumsum(np.array(dlen) - np.array(cached))])
+                        ref = oracle.forward_prefill(q_rot, None, None, kp, vp, offs,
+                                                     [table[r, :d] for r, d in zip(rows, dlen)], 128**-0.5)
+                    else:
+                        kvi, mask = oracle.naive_decode_metadata(table, rows, dlen)
+                        ref = oracle.naive_forward_decode(q_rot, kp, vp, kvi, mask, 128**-0.5)
+                    assert_close(o.view(t, 16, 128), ref, dt, f"fp8 backend {phase} {layer}")
+            for r in reqs:
+                r.complete_one()
+    finally:
+        set_global_ctx(None)
