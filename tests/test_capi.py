@@ -142,6 +142,32 @@ def test_host_side_argument_errors():
     assert rs(kp=nul) == _lib.MSGL_ERR_INVALID and "pools" in _lib.last_error()
     assert rs(slots=0) == _lib.MSGL_ERR_INVALID
     assert rs(hkv=0) == _lib.MSGL_ERR_INVALID
+    # fp8 store: (k, v, out_loc, k_pool, v_pool, kv_scale, T, Hkv, D, slots, dtype, stream)
+    sf = lambda t=4, d=128, dtype=1, sc=16, slots=100: lib.msgl_store_kv_fp8(  # noqa: E731
+        16, 16, 16, 16, 16, sc, t, 8, d, slots, dtype, nul)
+    assert sf(t=0) == _lib.MSGL_OK
+    assert sf(d=96) == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
+    assert sf(d=2048) == _lib.MSGL_ERR_UNSUPPORTED  # a row wider than one wavefront
+    assert sf(dtype=7) == _lib.MSGL_ERR_UNSUPPORTED
+    assert sf(sc=nul) == _lib.MSGL_ERR_INVALID
+    assert sf(sc=12) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
+    assert sf(slots=0) == _lib.MSGL_ERR_INVALID
+    # fp8 decode: (q, kp, vp, kv_scale, indptr, indices, seq_lens, B, Hq, Hkv, D, page, slots, dtype, scale,
+    #              splits, out, ws, ws_bytes, stream)
+    df = lambda dtype=1, hq=16, sc=16, d=128: lib.msgl_paged_decode_fp8(  # noqa: E731
+        16, 16, 16, sc, 16, 16, nul, 4, hq, 8, d, 1, 100, dtype, 0.1, 1, 16, 256, 1 << 30, nul)
+    assert df(sc=nul) == _lib.MSGL_ERR_INVALID and "kv_scale" in _lib.last_error()
+    assert df(dtype=0) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()  # fp32 q over fp8 pools
+    assert df(hq=128) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()  # group 16
+    assert df(d=96) == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
+    assert df(sc=12) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
+    # fp8 prefill: (q, kp, vp, kv_scale, q_indptr, kv_indptr, kv_indices, seq_lens, R, T, maxE, maxL, Hq, Hkv, D,
+    #               page, slots, dtype, scale, splits, out, ws, ws_bytes, stream)
+    pf8 = lambda dtype=1, sc=16, d=128: lib.msgl_prefill_ragged_fp8(  # noqa: E731
+        16, 16, 16, sc, 16, 16, 16, nul, 2, 64, 32, 0, 16, 8, d, 1, 100, dtype, 0.1, 1, 16, 256, 1 << 30, nul)
+    assert pf8(sc=nul) == _lib.MSGL_ERR_INVALID and "kv_scale" in _lib.last_error()
+    assert pf8(dtype=0) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()
+    assert pf8(d=96) == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
     # store_kv: zero tokens is a no-op; bad row size is unsupported
     assert lib.msgl_store_kv(nul, nul, nul, nul, nul, 0, 8, 128, 10, 1, nul) == _lib.MSGL_OK
     assert lib.msgl_store_kv(16, 16, 16, 16, 16, 4, 1, 3, 10, 1, nul) == _lib.MSGL_ERR_UNSUPPORTED
@@ -162,3 +188,21 @@ def test_python_wrapper_raises():
         ops.store_kv(torch.zeros(2, 4, 64), torch.zeros(2, 4, 64), torch.zeros(3, dtype=torch.int32), pool, pool)
     with pytest.raises(ValueError):
         _lib.dtype_code(torch.int8)
+    fp8 = torch.zeros(8, 4, 64, dtype=torch.float8_e4m3fn)
+    sc = torch.zeros(8, 4, 2)
+    k = torch.zeros(2, 4, 64, dtype=torch.bfloat16)
+    with pytest.raises(ValueError):  # pools must be fp8
+        ops.store_kv_fp8(k, k, torch.zeros(2, dtype=torch.int32), pool, pool, sc)
+    with pytest.raises(ValueError):  # kv_scale must be [N, Hkv, 2]
+        ops.store_kv_fp8(k, k, torch.zeros(2, dtype=torch.int32), fp8, fp8, torch.zeros(8, 4))
+    with pytest.raises(ValueError):  # fp8 pools need kv_scale
+        ops.paged_decode_attention(torch.zeros(2, 8, 64, dtype=torch.bfloat16), fp8, fp8,
+                                   torch.zeros(3, dtype=torch.int32), torch.zeros(2, dtype=torch.int32), 0.1)
+    with pytest.raises(ValueError):  # and 16-bit queries
+        ops.paged_decode_attention(torch.zeros(2, 8, 64), fp8, fp8, torch.zeros(3, dtype=torch.int32),
+                                   torch.zeros(2, dtype=torch.int32), 0.1, kv_scale=sc)
+    with pytest.raises(ValueError):  # rotary_dim / inv_freq mismatch
+        ops.rope(k, torch.zeros(2, dtype=torch.int32), torch.zeros(16), 64)
+    with pytest.raises(ValueError):  # the KV cache takes the model dtype or fp8 only
+        from minisgl_hip.kvcache import MHAKVCache
+        MHAKVCache(1, 8, 4, 64, torch.bfloat16, "cpu", kv_dtype=torch.float16)
