@@ -357,12 +357,6 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
 #pragma unroll
     for (int j = 0; j < NQF; ++j) qf[j] = ld16(qrow + (16 * j + 8 * h) * 2);
   }
-  // Q must have arrived before the key loop: otherwise the compiler's wait for
-  // it lands inside the loop (its wait analysis merges the loop entry), where a
-  // vmcnt would also drain the LDS transfers in flight.
-#pragma unroll
-  for (int j = 0; j < NQF; ++j) asm volatile("" ::"v"(qf[j]));
-
   // O accumulators: acc[dt][i] = O[row 8(i/4) + 4h + i%4][column 32 dt + rl]
   f32x16 acc[NDT];
 #pragma unroll
@@ -597,7 +591,32 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
     const int ntiles = (nw + KT - 1) / KT;
     const int kend = w0 + nw;
     __syncthreads();  // every wavefront is done with the previous window
-    for (int i = tid; i < nw; i += THREADS16) slots[i] = (int)kv_slot(p, kv_start, w0 + i);
+    {  // the window's slots: every gather load in flight before the first LDS store
+      constexpr int SPT = kWin / THREADS16;
+      int sv[SPT];
+#pragma unroll
+      for (int k = 0; k < SPT; ++k) {  // kv_slot in two passes: every load before any use
+        const int tok = w0 + min(tid + k * THREADS16, nw - 1);
+        sv[k] = p.kv_indices[kv_start + (p.page_size == 1 ? tok : tok / p.page_size)];
+      }
+#pragma unroll
+      for (int k = 0; k < SPT; ++k) {
+        const int tok = w0 + min(tid + k * THREADS16, nw - 1);
+        const int64_t sl = p.page_size == 1 ? (int64_t)sv[k] : (int64_t)sv[k] * p.page_size + tok % p.page_size;
+        sv[k] = (sl >= 0 && sl < p.num_slots) ? (int)sl : 0;
+      }
+#pragma unroll
+      for (int k = 0; k < SPT; ++k) {
+        const int i = tid + k * THREADS16;
+        if (i < nw) slots[i] = sv[k];
+      }
+    }
+    // Q must have arrived before the key loop: otherwise the compiler's wait
+    // for it lands inside the loop (its wait analysis merges the loop entry),
+    // where a vmcnt would also drain the LDS transfers in flight. Waiting here,
+    // with the first window's slot gather, makes the two share a round trip.
+#pragma unroll
+    for (int j = 0; j < NQF; ++j) asm volatile("" ::"v"(qf[j]));
     __syncthreads();
 #pragma unroll
     for (int s = 0; s < 2; ++s)
