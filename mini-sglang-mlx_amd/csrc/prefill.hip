@@ -81,8 +81,10 @@ struct PrefillParams {
   void* out;
   float* part_o;     // [splits][num_tokens][hq][D]
   float2* part_ml;   // [splits][num_tokens][hq]
-  int4* plan;        // work list: (request, kv head, query block, chunk), longest first
+  int4* plan;        // work list, longest first: per item (request, kv head, query block, chunk)
+                     // then (first token, extend length E, first kv index, kv length L)
   int* plan_count;   // its length
+  int* merge_n;      // [num_tokens] chunks of each token's block (<= 1: nothing to merge)
   int64_t num_slots;
   int hq, hkv, page_size;
   int num_reqs, num_tokens;
@@ -320,15 +322,12 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
 
   // ---- work item from the plan (workgroups past its end have nothing to do) ----
   if ((int)blockIdx.x >= *p.plan_count) return;
-  const int4 item = p.plan[blockIdx.x];
-  const int req = item.x, kvh = item.y, qblk = item.z, split = item.w;
-
-  const int q0 = p.q_indptr[req];
-  const int E = p.q_indptr[req + 1] - q0;
+  const int4 item = p.plan[2 * blockIdx.x];
+  const int4 geo = p.plan[2 * blockIdx.x + 1];  // the request's geometry, loaded with the item
+  const int kvh = item.y, qblk = item.z, split = item.w;
+  const int q0 = geo.x, E = geo.y, kv_start = geo.z, L = geo.w;
   const int qb = qblk * BQ;
   if (qb >= E) return;
-  const int kv_start = p.kv_indptr[req];
-  const int L = p.seq_lens ? p.seq_lens[req] : (p.kv_indptr[req + 1] - kv_start);
   const int P = L - E;
   const int kv_end = block_kv_end(L, E, qb, BQ);
   int nchunks, clen;
@@ -763,56 +762,92 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillParam
     const int n = plan_tiles(p, bq, t, req, qblk, split);
     if (n > 0) {
       const int pos = atomicAdd(&hist[min(n, 255)], 1);
-      for (int h = 0; h < p.hkv; ++h) p.plan[pos * p.hkv + h] = make_int4(req, h, qblk, split);
+      const int q0 = p.q_indptr[req];
+      const int kv0 = p.kv_indptr[req];
+      const int L = p.seq_lens ? p.seq_lens[req] : (p.kv_indptr[req + 1] - kv0);
+      const int4 geo = make_int4(q0, p.q_indptr[req + 1] - q0, kv0, L);
+      for (int h = 0; h < p.hkv; ++h) {
+        p.plan[2 * (pos * p.hkv + h)] = make_int4(req, h, qblk, split);
+        p.plan[2 * (pos * p.hkv + h) + 1] = geo;
+      }
+    }
+  }
+  if (p.splits > 1) {  // chunk count of every token's block, for the merge
+    for (int tk = threadIdx.x; tk < p.num_tokens; tk += kPlanThreads) {
+      int lo = 0, hi = p.num_reqs - 1;  // the last request r with q_indptr[r] <= tk
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (p.q_indptr[mid] <= tk) lo = mid; else hi = mid - 1;
+      }
+      const int q0 = p.q_indptr[lo];
+      const int E = p.q_indptr[lo + 1] - q0;
+      const int tok = tk - q0;
+      int n = 0, clen;
+      if (tok >= 0 && tok < E) {
+        const int L = p.seq_lens ? p.seq_lens[lo] : (p.kv_indptr[lo + 1] - p.kv_indptr[lo]);
+        chunk_geometry(block_kv_end(L, E, tok / bq * bq, bq), p.splits, p.chunk_len, n, clen);
+      }
+      p.merge_n[tk] = n;
     }
   }
 }
 
 // Combines the chunks of every query row whose block was split: one thread
-// per 4 output columns of one (token, head).
+// per 4 output columns of one (token, head). The plan kernel left each token's
+// chunk count in merge_n, so the (m, l) and O partials of up to kMergeUnroll
+// chunks are loaded at once, with no lookup in front of them.
+constexpr int kMergeUnroll = 4;
+
 template <typename T, int D>
-__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p, int bq) {
+__global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillParams p) {
   constexpr int TPH = D / 4;
   constexpr int HPB = 256 / TPH;
   const int tk = blockIdx.x;
+  const int n = p.merge_n[tk];
+  if (n <= 1) return;  // written by the attention kernel (or not a token of any request)
   const int h = blockIdx.y * HPB + threadIdx.x / TPH;
   const int d = (threadIdx.x % TPH) * 4;
   if (h >= p.hq) return;
-  // request owning token tk: the last r with q_indptr[r] <= tk
-  int lo = 0, hi = p.num_reqs - 1;
-  while (lo < hi) {
-    const int mid = (lo + hi + 1) >> 1;
-    if (p.q_indptr[mid] <= tk) lo = mid; else hi = mid - 1;
-  }
-  const int q0 = p.q_indptr[lo];
-  const int E = p.q_indptr[lo + 1] - q0;
-  const int L = p.seq_lens ? p.seq_lens[lo] : (p.kv_indptr[lo + 1] - p.kv_indptr[lo]);
-  const int tok = tk - q0;
-  if (tok < 0 || tok >= E) return;
-  const int kv_end = block_kv_end(L, E, tok / bq * bq, bq);
-  int n, clen;
-  chunk_geometry(kv_end, p.splits, p.chunk_len, n, clen);
-  if (n <= 1) return;  // written by the attention kernel
   const int64_t stride = (int64_t)p.num_tokens * p.hq;
   const int64_t idx = (int64_t)tk * p.hq + h;
-  float M = -INFINITY;
-  for (int c = 0; c < n; ++c) M = fmaxf(M, p.part_ml[c * stride + idx].x);
+  // out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c over the chunks, M = max_c m_c
+  // (kMergeUnroll chunks per pass, the running M rescaling earlier passes)
+  float M = -INFINITY, lsum = 0.f;
   float o[4] = {0.f, 0.f, 0.f, 0.f};
-  float lsum = 0.f;
-  for (int c = 0; c < n; ++c) {
-    const float2 ml = p.part_ml[c * stride + idx];
-    const float w = ml.x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml.x - M);
-    lsum += ml.y * w;
-    const float4 v = *reinterpret_cast<const float4*>(p.part_o + (c * stride + idx) * D + d);
-    o[0] += w * v.x;
-    o[1] += w * v.y;
-    o[2] += w * v.z;
-    o[3] += w * v.w;
+  for (int c0 = 0; c0 < n; c0 += kMergeUnroll) {
+    float2 ml[kMergeUnroll];
+    float4 v[kMergeUnroll];
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const int64_t e = (int64_t)min(c0 + u, n - 1) * stride + idx;
+      ml[u] = p.part_ml[e];
+      v[u] = *reinterpret_cast<const float4*>(p.part_o + e * D + d);
+      if (c0 + u >= n) ml[u] = make_float2(-INFINITY, 0.f);
+    }
+    float Mn = M;
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) Mn = fmaxf(Mn, ml[u].x);
+    const float a = M == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(M - Mn);
+    lsum *= a;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) o[e] *= a;
+#pragma unroll
+    for (int u = 0; u < kMergeUnroll; ++u) {
+      const float w = ml[u].x == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(ml[u].x - Mn);
+      lsum += ml[u].y * w;
+      o[0] += w * v[u].x;
+      o[1] += w * v[u].y;
+      o[2] += w * v[u].z;
+      o[3] += w * v[u].w;
+    }
+    M = Mn;
   }
   const float inv = 1.f / lsum;
   T* dst = reinterpret_cast<T*>(p.out) + idx * D + d;
+  T r[4];
 #pragma unroll
-  for (int e = 0; e < 4; ++e) dst[e] = from_f32<T>(o[e] * inv);
+  for (int e = 0; e < 4; ++e) r[e] = from_f32<T>(o[e] * inv);
+  *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(r);
 }
 
 // ---------------------------------------------------------------------------
@@ -1056,7 +1091,7 @@ int launch16(PrefillParams p, int max_e, hipStream_t stream) {
   if (p.splits > 1) {
     constexpr int HPB = 256 / (D / 4);
     hipLaunchKernelGGL((prefill_merge_kernel<T, D>), dim3(p.num_tokens, (p.hq + HPB - 1) / HPB), dim3(256), 0,
-                       stream, p, BQ);
+                       stream, p);
     MSGL_CHECK_LAUNCH("msgl_prefill_ragged (merge)");
   }
   return MSGL_OK;
@@ -1110,10 +1145,11 @@ int prefill_dim(const PrefillParams& p, int max_e, int head_dim, int group, hipS
 
 inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
-// Workspace of the 16-bit path: plan length, plan (one int4 per work item),
-// then with splits > 1 the per-chunk (m, l) and O partials.
+// Workspace of the 16-bit path: plan length, plan (two int4 per work item),
+// then with splits > 1 each token's chunk count and the per-chunk (m, l) and O
+// partials.
 struct PrefillWorkspace {
-  int64_t items, plan, part_ml, part_o, bytes;
+  int64_t items, plan, merge_n, part_ml, part_o, bytes;
 };
 PrefillWorkspace prefill_workspace(int num_reqs, int num_tokens, int max_e, int hq, int hkv, int head_dim,
                                    int splits) {
@@ -1122,7 +1158,8 @@ PrefillWorkspace prefill_workspace(int num_reqs, int num_tokens, int max_e, int 
   w.items = (int64_t)num_reqs * ((max_e + bq - 1) / bq) * splits * hkv;
   const int64_t rows = splits > 1 ? (int64_t)splits * num_tokens * hq : 0;
   w.plan = 256;
-  w.part_ml = w.plan + align256(w.items * 16);
+  w.merge_n = w.plan + align256(w.items * 32);
+  w.part_ml = w.merge_n + align256(splits > 1 ? (int64_t)num_tokens * 4 : 0);
   w.part_o = w.part_ml + align256(rows * 8);
   w.bytes = w.part_o + align256(rows * head_dim * 4);
   return w;
@@ -1203,6 +1240,7 @@ int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, co
   p.part_ml = nullptr;
   p.plan = nullptr;
   p.plan_count = nullptr;
+  p.merge_n = nullptr;
   p.plan_capacity = 0;
   p.num_slots = num_slots;
   p.hq = num_qo_heads;
@@ -1235,6 +1273,7 @@ int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, co
     p.plan = reinterpret_cast<int4*>(ws + w.plan);
     p.plan_capacity = (int)w.items;
     if (p.splits > 1) {
+      p.merge_n = reinterpret_cast<int*>(ws + w.merge_n);
       p.part_ml = reinterpret_cast<float2*>(ws + w.part_ml);
       p.part_o = reinterpret_cast<float*>(ws + w.part_o);
     }

@@ -57,10 +57,11 @@ def test_prefill_sizes():
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     # (R, T, maxE, Hq, Hkv, D, splits): 128 query rows per work item, so 64 tokens at Hq/Hkv = 2
     items = 16 * 8 * 8  # requests x query blocks (ceil(512 / 64)) x kv heads
-    assert lib.msgl_prefill_workspace_size(16, 2048, 512, 16, 8, 128, 1) == 256 + up(items * 16)
+    # work item = two int4 (item, request geometry); with splits > 1 a chunk count per token, then partials
+    assert lib.msgl_prefill_workspace_size(16, 2048, 512, 16, 8, 128, 1) == 256 + up(items * 32)
     rows = 4 * 2048 * 16
     assert lib.msgl_prefill_workspace_size(16, 2048, 512, 16, 8, 128, 4) == (
-        256 + up(4 * items * 16) + up(rows * 8) + up(rows * 128 * 4))
+        256 + up(4 * items * 32) + up(2048 * 4) + up(rows * 8) + up(rows * 128 * 4))
     assert lib.msgl_prefill_workspace_size(16, 2048, 512, 16, 6, 128, 4) == 0  # Hq not a multiple of Hkv
     # 16 requests x 8 kv heads x ceil(512 / 64) blocks = 1024 workgroups: two chunks reach 1536
     assert lib.msgl_prefill_default_splits(16, 16, 8, 128, 512, 4096) == 2
