@@ -239,6 +239,11 @@ struct MMA32<bf16_t> {
   __device__ __forceinline__ static uint32_t scale2(uint32_t w, float a) {
     return pack2(__uint_as_float(w << 16) * a, __uint_as_float(w & 0xffff0000u) * a);
   }
+  // acc + the two packed values (v_dot2c_f32_bf16 with (1, 1))
+  __device__ __forceinline__ static float sum2(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2_t, w), bf16x2_t{(__bf16)1.f, (__bf16)1.f}, acc,
+                                           false);
+  }
 };
 template <>
 struct MMA32<f16_t> {
@@ -252,6 +257,9 @@ struct MMA32<f16_t> {
   __device__ __forceinline__ static uint32_t scale2(uint32_t w, float a) {
     const f16x2_t v = __builtin_bit_cast(f16x2_t, w);
     return pack2((float)v[0] * a, (float)v[1] * a);
+  }
+  __device__ __forceinline__ static float sum2(uint32_t w, float acc) {
+    return __builtin_amdgcn_fdot2(__builtin_bit_cast(f16x2_t, w), f16x2_t{(_Float16)1.f, (_Float16)1.f}, acc, false);
   }
 };
 
@@ -283,20 +291,6 @@ struct G16 {
 // consecutive rows place one logical chunk in 16 different bank groups, and
 // rows 4g..4g+3 x chunks {2t, 2t+1} land in 8 different ones.
 __device__ __forceinline__ int swz(int r) { return ((r & 3) << 1) | (((r >> 2) & 1) << 3) | ((r >> 3) & 1); }
-
-// Instruction order hint for a basic block: DS LDS reads first, then NM MFMAs
-// each followed by VPM VALU instructions of the same wavefront, so the matrix
-// pipe and the VALU run concurrently (a run of MFMAs would block the
-// wavefront's issue until the pipe drains).
-template <int DS, int NM, int VPM>
-__device__ __forceinline__ void sched_interleave() {
-  __builtin_amdgcn_sched_group_barrier(0x100, DS, 0);
-#pragma unroll
-  for (int k = 0; k < NM; ++k) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-    __builtin_amdgcn_sched_group_barrier(0x002, VPM, 0);
-  }
-}
 
 // KV: the pools' storage type, T itself or fp8e4m3 (codes plus the per-slot,
 // per-kv-head (K, V) scales of p.kv_scale).
@@ -399,7 +393,8 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
     const uint32_t sb = lds0 + st * Geo::STAGE_BYTES;
 #pragma unroll
     for (int i = 0; i < IPW; ++i) {
-      const uint8_t* g = kcol[i] + (int64_t)nslot[i] * row_stride;
+      // slots are clamped into [0, num_slots) and a row stride fits 32 bits: one 32 x 32 -> 64-bit multiply-add
+      const uint8_t* g = kcol[i] + (uint64_t)(uint32_t)nslot[i] * (uint32_t)row_stride;
       if (kv_issuer) {
         const uint32_t lk = __builtin_amdgcn_readfirstlane(sb + (wave + NWAVE16 * i) * 1024);
         dma16(g, lk);
@@ -422,29 +417,41 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
     }
   };
 
-  // S^T = K Q^T of the tile in ring stage st: lane l gets the scores of row rl
-  // against keys 8c + 4h + r (c, r = 0..3) in sdst[4c + r]
-  // (two independent MFMA chains over even and odd d steps, summed)
-  auto scores = [&](int st, f32x16& sdst) {
-    const uint8_t* krow = smem + st * Geo::STAGE_BYTES + rl * RBYTES;  // A operand: key row rl
+  // K operands (A of S^T = K Q^T) of the tile in stage st, all read before
+  // the first MFMA: d step j takes key row rl, d = 16j + 8h .. +7 (fp8: half h
+  // of chunk j, widened when used)
+  struct KOps {
+    u32x4 w[Q8 ? 1 : NQF];
+    uint2 b[Q8 ? NQF : 1];
+  };
+  auto k_read = [&](int st, KOps& ko) {
+    const uint8_t* krow = smem + st * Geo::STAGE_BYTES + rl * RBYTES;
     const int sw = swz(rl) & SWZ;
-    f32x16 s2[2];
-#pragma unroll
-    for (int c = 0; c < 2; ++c)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) s2[c][i] = 0.f;
 #pragma unroll
     for (int j = 0; j < NQF; ++j) {
-      u32x4 a;
-      if constexpr (Q8) {  // d 16j + 8h .. +7 = half h of chunk j
-        const uint2 k8 = *reinterpret_cast<const uint2*>(krow + ((j ^ sw) << 4) + 8 * h);
-        a = fp8x8<T>(k8.x, k8.y);
+      if constexpr (Q8) {
+        ko.b[j] = *reinterpret_cast<const uint2*>(krow + ((j ^ sw) << 4) + 8 * h);
       } else {
-        a = *reinterpret_cast<const u32x4*>(krow + (((2 * j + h) ^ sw) << 4));
+        ko.w[j] = *reinterpret_cast<const u32x4*>(krow + (((2 * j + h) ^ sw) << 4));
       }
-      s2[j & 1] = MMA32<T>::mma(a, qf[j], s2[j & 1]);
     }
-    sdst = s2[0] + s2[1];
+  };
+  auto k_operand = [&](const KOps& ko, int j) -> u32x4 {
+    if constexpr (Q8) {
+      return fp8x8<T>(ko.b[j].x, ko.b[j].y);
+    } else {
+      return ko.w[j];
+    }
+  };
+  // S^T = K Q^T of the tile in ring stage st: lane l gets the scores of row rl
+  // against keys 8c + 4h + r (c, r = 0..3) in sdst[4c + r] (one MFMA chain over d)
+  auto scores = [&](int st, f32x16& sdst) {
+    KOps ko;
+    k_read(st, ko);
+    f32x16 acc_s = {};
+#pragma unroll
+    for (int j = 0; j < NQF; ++j) acc_s = MMA32<T>::mma(k_operand(ko, j), qf[j], acc_s);
+    sdst = acc_s;
   };
   // Row max of the scores of tile t (keys kbase..), raw (scale > 0, so the raw
   // max orders like the scaled one); x gets the scores, -inf where masked.
@@ -460,49 +467,35 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
       for (int r = 0; r < 4; ++r) sc[4 * c + r] = a[r];
     }
   };
-  // (a quantised key's scale multiplies its score; ks is unused otherwise)
-  auto rowmax_full = [&](const f32x16& sc, const float (&ks)[16], float (&x)[16]) {
+  // Block A of an iteration: the S^T MFMAs of the tile in stage st (one chain
+  // over d) with the row max of the current tile's scores sc between them,
+  // 16 / NQF scores per MFMA, in this order (sched_barrier: the matrix core
+  // runs each MFMA while the wavefront issues the VALU work behind it).
+  // x gets the scores (a quantised key's scale applied), -inf where masked:
+  // key 8(i/4) + 4h + i%4 of the tile is visible iff it is <= thr.
+  auto scores_rowmax = [&](int st, f32x16& sdst, const f32x16& sc, const float (&ks)[16], float (&x)[16], int thr,
+                           auto masked) -> float {
+    constexpr bool MASKED = decltype(masked)::value;
+    constexpr int EPM = 16 / NQF;
+    KOps ko;
+    k_read(st, ko);
     float m = -INFINITY;
+    f32x16 acc_s = {};
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      x[i] = Q8 ? sc[i] * ks[i] : sc[i];
-      m = fmaxf(m, x[i]);
+    for (int j = 0; j < NQF; ++j) {
+      acc_s = MMA32<T>::mma(k_operand(ko, j), qf[j], acc_s);
+#pragma unroll
+      for (int e = 0; e < EPM; ++e) {
+        const int i = j * EPM + e;
+        float v = Q8 ? sc[i] * ks[i] : sc[i];
+        if (MASKED && 8 * (i >> 2) + (i & 3) > thr) v = -INFINITY;
+        x[i] = v;
+        m = fmaxf(m, v);
+      }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    sdst = acc_s;
     return m;
-  };
-  auto rowmax_masked = [&](const f32x16& sc, const float (&ks)[16], float (&x)[16], int kbase, int kend) {
-    // key 8(i/4) + 4h + i%4 of the tile is visible iff it is <= thr
-    const int thr = min(limit, kend - 1) - kbase - 4 * h;
-    float m = -INFINITY;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      x[i] = 8 * (i >> 2) + (i & 3) <= thr ? (Q8 ? sc[i] * ks[i] : sc[i]) : -INFINITY;
-      m = fmaxf(m, x[i]);
-    }
-    return m;
-  };
-  // P = exp2(x * scale - m_run) into the A operands of the two 16-key steps of
-  // O += P V: slot (h, e) of step ks = key 16ks + 8(e/4) + 4h + e%4, i.e. this
-  // lane's scores 8ks .. 8ks+7 in order
-  // (fp8: a quantised V row's scale folds into its weight in P; l keeps the plain weights)
-  auto probs = [&](const float (&x)[16], const float (&vs)[16], u32x4 (&pa)[2]) {
-    const float m_use = m_run == -INFINITY ? 0.f : m_run;  // a row may see nothing yet
-    float pr[16];
-    float lsum = 0.f;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], p.scale_log2, -m_use));
-      lsum += pr[i];
-    }
-    l_run += lsum;
-    if (Q8) {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) pr[i] *= vs[i];
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int w = 0; w < 4; ++w) pa[ks][w] = MMA32<T>::pack2(pr[8 * ks + 2 * w], pr[8 * ks + 2 * w + 1]);
   };
   // Lazy rescale: a row's reference m_run (log2 domain) moves only when its max
   // exceeds it by more than 8, so P <= 2^8 and most tiles leave the
@@ -576,6 +569,79 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
       }
     }
   };
+  // Block C: O += P V for the tile in stage st (MFMA k: 16-key step k / NDT,
+  // column tile k % NDT, so consecutive MFMAs are independent) with this
+  // tile's P = exp2(x * scale - m_run) between them, 16 / (2 NDT) keys per
+  // MFMA, packed into the A operands of the next P V (slot (h, e) of step ks =
+  // key 16ks + 8(e/4) + 4h + e%4, i.e. this lane's scores 8ks .. 8ks+7 in order).
+  // fp8: a quantised V row's scale folds into its weight in P; l keeps the plain weights.
+  auto pv_probs = [&](int st, const u32x4 (&pa)[2], const float (&x)[16], const float (&vs)[16],
+                      u32x4 (&pa_new)[2], auto do_pv) {
+    constexpr bool DO_PV = decltype(do_pv)::value;
+    constexpr int NMF = 2 * NDT;
+    constexpr int EPM = 16 / NMF;
+    const uint8_t* Vb = smem + st * Geo::STAGE_BYTES + Geo::TILE_BYTES;
+    const int i16 = lane & 15;
+    const int gs = (lane >> 4) & 1;
+    // B operands, read in the order of use (layouts as in pv)
+    u32x4 bop[2][NDT];
+    uint2 b8[2][NDT];
+    if constexpr (DO_PV) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        if constexpr (Q8) {
+          const int r = 16 * ks + 8 * (i16 >> 3) + 4 * h + ((i16 >> 1) & 3);
+          const uint8_t* vr = Vb + r * RBYTES + ((i16 & 1) << 3);
+          const int sw = swz(r) & SWZ;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) b8[ks][dt] = lds_read_tr8(vr + (((2 * dt + gs) ^ sw) << 4));
+        } else {
+          const int r0 = 16 * ks + 4 * h + (i16 >> 2);
+          const uint8_t* v0 = Vb + r0 * RBYTES + ((i16 & 1) << 3);
+          const uint8_t* v1 = v0 + 8 * RBYTES;
+          const int sw0 = swz(r0) & SWZ, sw1 = swz(r0 + 8) & SWZ;
+#pragma unroll
+          for (int dt = 0; dt < NDT; ++dt) {
+            const int c = 4 * dt + 2 * gs + ((i16 & 3) >> 1);
+            const uint2 lo = lds_read_tr16<T>(v0 + ((c ^ sw0) << 4));
+            const uint2 hi = lds_read_tr16<T>(v1 + ((c ^ sw1) << 4));
+            bop[ks][dt] = u32x4{lo.x, lo.y, hi.x, hi.y};
+          }
+        }
+      }
+    }
+    const float m_use = m_run == -INFINITY ? 0.f : m_run;  // a row may see nothing yet
+    float pr[16];
+    float ls[2] = {0.f, 0.f};  // fp8: the row sum of the plain weights (P carries the V scales)
+    float lp = 0.f;            // otherwise: of the rounded weights the P V products use
+#pragma unroll
+    for (int k = 0; k < NMF; ++k) {
+      if constexpr (DO_PV) {
+        const int ks = k / NDT, dt = k % NDT;
+        if constexpr (Q8) {
+          acc[dt] = MMA32<T>::mma(pa[ks], fp8x8<T>(b8[ks][dt].x, b8[ks][dt].y), acc[dt]);
+        } else {
+          acc[dt] = MMA32<T>::mma(pa[ks], bop[ks][dt], acc[dt]);
+        }
+      }
+#pragma unroll
+      for (int e = 0; e < EPM; ++e) {
+        const int i = k * EPM + e;
+        pr[i] = __builtin_amdgcn_exp2f(__builtin_fmaf(x[i], p.scale_log2, -m_use));
+        if (Q8) {
+          ls[i & 1] += pr[i];
+          pr[i] *= vs[i];
+        }
+        if (i & 1) {
+          const uint32_t w = MMA32<T>::pack2(pr[i - 1], pr[i]);
+          pa_new[i >> 3][(i & 7) >> 1] = w;
+          if (!Q8) lp = MMA32<T>::sum2(w, lp);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l_run += Q8 ? ls[0] + ls[1] : lp;
+  };
   // Software pipeline per window, three tiles deep. Iteration t:
   //   A: the S MFMAs of tile t+1 interleaved with tile t's masked row max;
   //   B: (rare) the rescale when a row's max moved;
@@ -641,29 +707,22 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
       float x[16];
       float ksc[16];  // fp8: tile t's K scales
       if constexpr (Q8) tile_scales(t % NS, 0, ksc);
-      constexpr int ADS = Q8 ? NQF + 4 : NQF;  // LDS reads of block A
       float mloc;
       if (kbase + KT <= kend && kbase + KT - 1 <= lim_lo) {
-        scores((t + 1) % NS, s_next);
-        mloc = rowmax_full(s_cur, ksc, x);
-        sched_interleave<ADS, NQF, 2>();
+        mloc = scores_rowmax((t + 1) % NS, s_next, s_cur, ksc, x, 0, std::false_type{});
       } else {
-        scores((t + 1) % NS, s_next);
-        mloc = rowmax_masked(s_cur, ksc, x, kbase, kend);
-        sched_interleave<ADS, NQF, 4>();
+        mloc = scores_rowmax((t + 1) % NS, s_next, s_cur, ksc, x, min(limit, kend - 1) - kbase - 4 * h,
+                             std::true_type{});
       }
       mloc = xor32_max(mloc);  // with the row's other 16 keys
       // B
       rescale(mloc, pa_prev, !FIRST);
       // C
-      u32x4 pa_new[2];
-      if constexpr (!FIRST) pv((t - 1) % NS, pa_prev);
       float vsc[16];  // fp8: tile t's V scales
       if constexpr (Q8) tile_scales(t % NS, 1, vsc);
-      probs(x, vsc, pa_new);
       load_slots(t + 3, nw);  // for the next iteration's issue (clamped: harmless when unused)
-      constexpr int CDS = Q8 ? 2 * NDT + IPW + 1 + 4 : 4 * NDT + IPW;  // LDS reads of block C
-      if constexpr (!FIRST) sched_interleave<CDS, 2 * NDT, 6>();
+      u32x4 pa_new[2];
+      pv_probs((t - 1 + NS) % NS, pa_prev, x, vsc, pa_new, std::integral_constant<bool, !FIRST>{});
       pa_prev[0] = pa_new[0];
       pa_prev[1] = pa_new[1];
       s_cur = s_next;
