@@ -696,22 +696,30 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
     scores(0, s_cur);
     u32x4 pa_prev[2];
 
-    auto iteration = [&](int t, auto first) {
+    // stc: tile t's ring stage as a compile-time constant (the main loop runs
+    // NS iterations per trip, so every LDS address offset folds into the
+    // instructions), or -1 for one computed at run time
+    auto iteration = [&](int t, auto first, auto stc) {
       constexpr bool FIRST = decltype(first)::value;
+      constexpr int SC = decltype(stc)::value;
+      const int st = SC >= 0 ? SC : t % NS;
+      const int st1 = SC >= 0 ? (SC + 1) % NS : (t + 1) % NS;
+      const int st2 = SC >= 0 ? (SC + 2) % NS : (t + 2) % NS;
+      const int stp = SC >= 0 ? (SC + NS - 1) % NS : (t + NS - 1) % NS;
       if (t + 1 < ntiles) vm_wait<0>();  // tile t+1, the only one in flight, landed
       __syncthreads();  // tile t+1 visible; everyone is done with tile t-2's stage
-      if (t + 2 < ntiles) issue((t + 2) % NS);
+      if (t + 2 < ntiles) issue(st2);
       const int kbase = w0 + t * KT;
       // A (past the last tile, scores reads a stage whose transfers have all landed; unused)
       f32x16 s_next;
       float x[16];
       float ksc[16];  // fp8: tile t's K scales
-      if constexpr (Q8) tile_scales(t % NS, 0, ksc);
+      if constexpr (Q8) tile_scales(st, 0, ksc);
       float mloc;
       if (kbase + KT <= kend && kbase + KT - 1 <= lim_lo) {
-        mloc = scores_rowmax((t + 1) % NS, s_next, s_cur, ksc, x, 0, std::false_type{});
+        mloc = scores_rowmax(st1, s_next, s_cur, ksc, x, 0, std::false_type{});
       } else {
-        mloc = scores_rowmax((t + 1) % NS, s_next, s_cur, ksc, x, min(limit, kend - 1) - kbase - 4 * h,
+        mloc = scores_rowmax(st1, s_next, s_cur, ksc, x, min(limit, kend - 1) - kbase - 4 * h,
                              std::true_type{});
       }
       mloc = xor32_max(mloc);  // with the row's other 16 keys
@@ -719,16 +727,30 @@ __global__ __launch_bounds__(THREADS16) __attribute__((amdgpu_waves_per_eu(G16<D
       rescale(mloc, pa_prev, !FIRST);
       // C
       float vsc[16];  // fp8: tile t's V scales
-      if constexpr (Q8) tile_scales(t % NS, 1, vsc);
+      if constexpr (Q8) tile_scales(st, 1, vsc);
       load_slots(t + 3, nw);  // for the next iteration's issue (clamped: harmless when unused)
       u32x4 pa_new[2];
-      pv_probs((t - 1 + NS) % NS, pa_prev, x, vsc, pa_new, std::integral_constant<bool, !FIRST>{});
+      pv_probs(stp, pa_prev, x, vsc, pa_new, std::integral_constant<bool, !FIRST>{});
       pa_prev[0] = pa_new[0];
       pa_prev[1] = pa_new[1];
       s_cur = s_next;
     };
-    iteration(0, std::true_type{});
-    for (int t = 1; t < ntiles; ++t) iteration(t, std::false_type{});
+    static_assert(NS == 4, "the main loop is unrolled for a four-stage ring");
+    using C0 = std::integral_constant<int, 0>;
+    using C1 = std::integral_constant<int, 1>;
+    using C2 = std::integral_constant<int, 2>;
+    using C3 = std::integral_constant<int, 3>;
+    iteration(0, std::true_type{}, C0{});
+    int t = 1;
+    if constexpr (D <= 128) {  // (at 256 the unrolled body would spill)
+      for (; t + 3 < ntiles; t += 4) {  // tiles 1..4 mod 4: stages 1, 2, 3, 0
+        iteration(t, std::false_type{}, C1{});
+        iteration(t + 1, std::false_type{}, C2{});
+        iteration(t + 2, std::false_type{}, C3{});
+        iteration(t + 3, std::false_type{}, C0{});
+      }
+    }
+    for (; t < ntiles; ++t) iteration(t, std::false_type{}, std::integral_constant<int, -1>{});
     pv((ntiles - 1) % NS, pa_prev);
   }
 
