@@ -310,16 +310,17 @@ def bench_decode_fp8(args, dev):
     ws = ops.decode_workspace(BATCH, HQ, HKV, D, splits, dev)
 
     def run(i, ev):
-        # per step: one plan; per layer: quantising store of the new token, then fp8 decode + merge
+        # per step: one plan; per layer: the fp8 decode launch that quantises and
+        # stores the new token itself (msgl_paged_decode_store_fp8_planned), then the merge
         ops.paged_decode_plan(indptr, None, BATCH, HQ, HKV, D, splits, ws)
         timed = i % LAYERS
         for layer in range(LAYERS):
             kp, vp, sc = pools[layer]
             if ev and layer == timed:
                 ev[0].record()
-            ops.store_kv_fp8(ks[layer], vs[layer], out_loc, kp, vp, sc)
             ops.paged_decode_attention(qs[layer], kp, vp, indptr, indices, D**-0.5, max_splits=splits,
-                                       out=outs[layer], workspace=ws, planned=True, kv_scale=sc)
+                                       out=outs[layer], workspace=ws, planned=True, kv_scale=sc,
+                                       new_kv=(ks[layer], vs[layer], out_loc))
             if ev and layer == timed:
                 ev[1].record()
 
@@ -332,7 +333,7 @@ def bench_decode_fp8(args, dev):
         "paged decode over fp8 e4m3 pools (one fp32 scale per slot and kv head), Qwen3-0.6B attention (16 q / 8 kv "
         "heads, head_dim 128), 28 layers; batch 128, context U[200,2048] (seed 0), page_size 1, 262144-slot pools "
         "quantised from N(0,1) bf16 rows, random slots; per step: one plan; per layer: quantising store of the new "
-        "token + fp8 paged decode + split-K merge",
+        "token fused into the fp8 paged decode launch + split-K merge",
         {"batch": BATCH, "sum_context": sum_l, "layers": LAYERS, "max_splits": splits,
          "bytes_per_layer": dec_bytes + store_bytes, "us_per_layer": round(sec * 1e6 / LAYERS, 2),
          "store_decode_merge_us": round(ev_s * 1e6, 2)},

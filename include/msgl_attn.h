@@ -24,6 +24,7 @@
  *   msgl_rope_store_kv       layers.py:107-109 (rotate q and k, then store_kv) in one launch
  *   msgl_store_kv_fp8,       the fp8 KV cache of docs/09-exercises.md:81-82 (store_kv and paged
  *   msgl_paged_decode_fp8,   decode over pools of e4m3 codes with one scale per slot and kv head,
+ *   msgl_paged_decode_store_fp8  the two in one launch,
  *   msgl_prefill_ragged_fp8  and the ragged prefill over them)
  *
  * Layouts (identical to the reference, no transposes at the boundary):
@@ -309,7 +310,7 @@ int msgl_store_kv_fp8(const void* k, const void* v, const int32_t* out_loc, void
  * Same workspace (msgl_paged_decode_workspace_size) and plan
  * (msgl_paged_decode_plan) as the unquantised decode; the _planned form skips
  * the plan like msgl_paged_decode_planned. The new token is stored first with
- * msgl_store_kv_fp8 (there is no fused-store form).
+ * msgl_store_kv_fp8, or by the _store_fp8 forms below.
  */
 int msgl_paged_decode_fp8(const void* q, const void* k_pool, const void* v_pool, const float* kv_scale,
                           const int32_t* kv_indptr, const int32_t* kv_indices,
@@ -322,6 +323,30 @@ int msgl_paged_decode_fp8_planned(const void* q, const void* k_pool, const void*
                                   int32_t head_dim, int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
                                   int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
                                   void* stream);
+
+/*
+ * msgl_store_kv_fp8(k_new, v_new, out_loc, ...) followed by
+ * msgl_paged_decode_fp8(...) in one decode launch (kvcache/pool.py:47-50 +
+ * attention/metal.py:112-131 over fp8 pools): the unit that holds request b's
+ * last position quantises its kv head's new K and V rows (k_new/v_new
+ * [B, Hkv, D] of q's dtype, 16-byte aligned) with the store's arithmetic, writes
+ * codes and scales at out_loc[b], then reads them back like every other token;
+ * pools and kv_scale end up bit-identical to the two-call sequence. _planned as
+ * msgl_paged_decode_fp8_planned.
+ */
+int msgl_paged_decode_store_fp8(const void* q, const void* k_new, const void* v_new, const int32_t* out_loc,
+                                void* k_pool, void* v_pool, float* kv_scale, const int32_t* kv_indptr,
+                                const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                                int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
+                                void* workspace, int64_t workspace_bytes, void* stream);
+int msgl_paged_decode_store_fp8_planned(const void* q, const void* k_new, const void* v_new, const int32_t* out_loc,
+                                        void* k_pool, void* v_pool, float* kv_scale, const int32_t* kv_indptr,
+                                        const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                                        int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                        int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                                        int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
+                                        void* stream);
 
 /*
  * msgl_prefill_ragged over fp8 pools (the same kv_scale [num_slots, Hkv, 2]

@@ -175,6 +175,36 @@ __device__ __forceinline__ float row16_sum(float v) {
   return v;
 }
 
+// OCP fp8 e4m3 quantisation of one row of a KV pool, shared by the
+// quantising store and the decode launch that stores the new token itself
+// (so both write the same codes): the row is lpr consecutive lanes, each
+// holding one 16-byte chunk `in` of VEC elements of T. amax = max |x| over the
+// row (lane exchanges), codes = e4m3(x * (448 / amax)) rounded to nearest even
+// into w (byte e of the chunk in byte e % 4 of w[e / 4]), +0 codes for a row
+// of zeros; the row's scale is amax / 448. Returns amax. Every lane of an
+// lpr-group must take part (the exchanges read its neighbours).
+template <typename T>
+__device__ __forceinline__ float fp8_quantize_chunk(const u32x4& in, int lpr, uint32_t (&w)[16 / sizeof(T) / 4]) {
+  constexpr int VEC = 16 / (int)sizeof(T);
+  float x[VEC];
+  Vec16<T>::to_f32(in, x);
+  float amax = 0.f;
+#pragma unroll
+  for (int e = 0; e < VEC; ++e) amax = fmaxf(amax, fabsf(x[e]));
+  for (int off = 1; off < lpr; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+  const float inv = amax > 0.f ? 448.f / amax : 0.f;
+#pragma unroll
+  for (int i = 0; i < VEC / 4; ++i) {
+    const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * i] * inv, x[4 * i + 1] * inv, 0, false);
+    w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[4 * i + 2] * inv, x[4 * i + 3] * inv, lo, true);
+  }
+  if (amax == 0.f) {
+#pragma unroll
+    for (int i = 0; i < VEC / 4; ++i) w[i] = 0u;  // +0 codes, also for -0 inputs
+  }
+  return amax;
+}
+
 // Ordering point for LDS traffic between lanes of one wavefront.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

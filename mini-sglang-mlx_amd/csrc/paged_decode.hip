@@ -141,6 +141,7 @@ struct DecodeParams {
   const void* k_pool;
   const void* v_pool;
   const float* kv_scale;  // fp8 pools: [num_slots, Hkv, 2] (K, V) scales per slot and kv head
+  float* kv_scale_w;      // the same, written by the fused store of an fp8 decode
   const int32_t* kv_indptr;
   const int32_t* kv_indices;
   const int32_t* seq_lens;
@@ -306,6 +307,33 @@ void paged_decode_kernel(DecodeParams p) {
         const int64_t dst = slot * row_stride + (int64_t)kvh * D * ES + vc * VEC * ES;
         st16(reinterpret_cast<uint8_t*>(p.k_pool_w) + dst, ld16(knew_p));
         st16(reinterpret_cast<uint8_t*>(p.v_pool_w) + dst, ld16(vnew_p));
+      }
+    }
+    // Fused store over fp8 pools: the chunk holding the new token quantises its
+    // K and V rows exactly like msgl_store_kv_fp8 (lanes [0, LQ) the K row,
+    // [LQ, 2 LQ) the V row, one 16-byte chunk of T each) and writes codes and
+    // scales before any load of the chunk is issued; the loop then reads the
+    // new token from the pool like every other token.
+    if constexpr (Q8) {
+      if (active && p.k_new != nullptr && t1 == L) {
+        constexpr int LQ = D / VEC;  // lanes per input row
+        static_assert(2 * LQ <= 64, "a wavefront quantises the K and V rows together");
+        const int sub = lane % LQ;
+        const bool is_v = (lane / LQ) & 1;  // lanes >= 2 LQ repeat the rows and write nothing
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(is_v ? p.v_new : p.k_new) +
+                             (((int64_t)b * p.hkv + kvh) * D + sub * VEC) * ES;
+        uint32_t w[VEC / 4];
+        const float amax = fp8_quantize_chunk<T>(ld16(src), LQ, w);
+        const int64_t slot = p.out_loc[b];
+        if (lane < 2 * LQ && slot >= 0 && slot < p.num_slots) {
+          uint8_t* dst = reinterpret_cast<uint8_t*>(is_v ? p.v_pool_w : p.k_pool_w) +
+                         (slot * p.hkv + kvh) * D + sub * VEC;
+          static_assert(VEC == 8, "16-bit queries: eight codes per lane");
+          *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+          if (sub == 0) p.kv_scale_w[(slot * p.hkv + kvh) * 2 + (is_v ? 1 : 0)] = amax / 448.f;
+        }
+        // the stores have completed before this wavefront loads the slot back
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
       }
     }
 
@@ -856,6 +884,44 @@ extern "C" int msgl_paged_decode_fp8_planned(const void* q, const void* k_pool, 
                            stream);
 }
 
+extern "C" int msgl_paged_decode_store_fp8(const void* q, const void* k_new, const void* v_new,
+                                           const int32_t* out_loc, void* k_pool, void* v_pool, float* kv_scale,
+                                           const int32_t* kv_indptr, const int32_t* kv_indices,
+                                           const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                           int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                           int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                                           void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(kv_scale != nullptr, "msgl_paged_decode_store_fp8: null kv_scale");
+  MSGL_CHECK_ARG(k_new && v_new && out_loc, "msgl_paged_decode_store_fp8: null k_new, v_new or out_loc");
+  MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
+                 "msgl_paged_decode_store_fp8: k_new and v_new must be 16-byte aligned");
+  return paged_decode_impl("msgl_paged_decode_store_fp8", kPlanAndRun, q, k_new, v_new, out_loc, k_pool, v_pool,
+                           kv_scale, kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim,
+                           page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream);
+}
+
+extern "C" int msgl_paged_decode_store_fp8_planned(const void* q, const void* k_new, const void* v_new,
+                                                   const int32_t* out_loc, void* k_pool, void* v_pool,
+                                                   float* kv_scale, const int32_t* kv_indptr,
+                                                   const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                                                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                                   int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                                                   int32_t max_splits, void* out, void* workspace,
+                                                   int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(kv_scale != nullptr, "msgl_paged_decode_store_fp8_planned: null kv_scale");
+  MSGL_CHECK_ARG(k_new && v_new && out_loc, "msgl_paged_decode_store_fp8_planned: null k_new, v_new or out_loc");
+  MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
+                 "msgl_paged_decode_store_fp8_planned: k_new and v_new must be 16-byte aligned");
+  return paged_decode_impl("msgl_paged_decode_store_fp8_planned", kRunPlanned, q, k_new, v_new, out_loc, k_pool,
+                           v_pool, kv_scale, kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads,
+                           head_dim, page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes,
+                           stream);
+}
+
 static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, const void* k_new, const void* v_new,
                              const int32_t* out_loc, const void* k_pool, const void* v_pool, const float* kv_scale,
                              const int32_t* kv_indptr, const int32_t* kv_indices,
@@ -905,6 +971,7 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
   p.out_loc = out_loc;
   p.k_pool_w = const_cast<void*>(k_pool);
   p.v_pool_w = const_cast<void*>(v_pool);
+  p.kv_scale_w = const_cast<float*>(kv_scale);
   const DecodeWorkspace w = decode_workspace(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   p.meta = reinterpret_cast<int*>(ws);

@@ -103,25 +103,10 @@ __global__ __launch_bounds__(256) void store_kv_fp8_kernel(const uint8_t* __rest
     const int64_t t = th / hkv;
     const int h = (int)(th - t * hkv);
     const uint8_t* src = (is_v ? v : k) + (th * head_dim + (int64_t)sub * VEC) * sizeof(T);
-    float x[VEC];
-    Vec16<T>::to_f32(ld16(src), x);
-    float amax = 0.f;
-#pragma unroll
-    for (int e = 0; e < VEC; ++e) amax = fmaxf(amax, fabsf(x[e]));
-    for (int off = 1; off < lpr; off <<= 1) amax = fmaxf(amax, __shfl_xor(amax, off));
+    uint32_t w[VEC / 4];
+    const float amax = fp8_quantize_chunk<T>(ld16(src), lpr, w);
     const int64_t slot = out_loc[t];
     if (slot < 0 || slot >= num_slots) continue;  // never write outside the pool (uniform per row)
-    const float inv = amax > 0.f ? 448.f / amax : 0.f;
-    uint32_t w[VEC / 4];
-#pragma unroll
-    for (int i = 0; i < VEC / 4; ++i) {
-      int lo = __builtin_amdgcn_cvt_pk_fp8_f32(x[4 * i] * inv, x[4 * i + 1] * inv, 0, false);
-      w[i] = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x[4 * i + 2] * inv, x[4 * i + 3] * inv, lo, true);
-    }
-    if (amax == 0.f) {
-#pragma unroll
-      for (int i = 0; i < VEC / 4; ++i) w[i] = 0u;  // +0 codes, also for -0 inputs
-    }
     uint8_t* dst = (is_v ? v_codes : k_codes) + (slot * hkv + h) * head_dim + (int64_t)sub * VEC;
     if constexpr (VEC == 8) {
       *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);

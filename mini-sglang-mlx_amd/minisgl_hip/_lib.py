@@ -125,6 +125,13 @@ SIGNATURES["msgl_prefill_plan"] = (
 )
 SIGNATURES["msgl_paged_decode_planned"] = SIGNATURES["msgl_paged_decode"]
 SIGNATURES["msgl_paged_decode_store_planned"] = SIGNATURES["msgl_paged_decode_store"]
+SIGNATURES["msgl_paged_decode_store_fp8"] = (
+    ctypes.c_int,
+    [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,  # q, k_new, v_new, out_loc, k_pool, v_pool, kv_scale
+     _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32,
+     _c_f, _c_i32, _c_p, _c_p, _c_i64, _c_p],
+)
+SIGNATURES["msgl_paged_decode_store_fp8_planned"] = SIGNATURES["msgl_paged_decode_store_fp8"]
 
 _lib = None
 

@@ -69,9 +69,8 @@ class HipAttnBackend(BaseAttnBackend):
     def __init__(self, config, kv_cache, page_table: np.ndarray, fuse_decode_store: bool = True) -> None:
         super().__init__(config, kv_cache, page_table)
         self.device = kv_cache.k[0].device
-        # an fp8 pool quantises in its own store: no fused store in the decode launch
-        self.fuse_decode_store = (fuse_decode_store and hasattr(kv_cache, "take_pending")
-                                  and not getattr(kv_cache, "quantized", False))
+        # (an fp8 pool's deferred store quantises inside the fp8 decode launch)
+        self.fuse_decode_store = fuse_decode_store and hasattr(kv_cache, "take_pending")
 
     def prepare_metadata(self, batch: "Batch") -> None:
         if self.fuse_decode_store:
@@ -114,8 +113,7 @@ class HipAttnBackend(BaseAttnBackend):
         ws = meta.workspace
         pending = self.kv_cache.take_pending(layer_id) if self.fuse_decode_store else None
         if pending is not None and pending[0].shape[0] != q.shape[0]:
-            k, v, out_loc = pending  # not one new token per request: store eagerly
-            ops.store_kv(k, v, out_loc, self.kv_cache.k[layer_id], self.kv_cache.v[layer_id])
+            self.kv_cache.store_now(*pending, layer_id)  # not one new token per request: store eagerly
             pending = None
         return ops.paged_decode_attention(
             q,

@@ -15,8 +15,9 @@ every reader still observes the pool exactly as after an eager store.
 
 fp8 pools (``kv_dtype=torch.float8_e4m3fn``, the extension docs/09-exercises.md:81-82
 describes): ``k``/``v`` hold e4m3 codes and ``kv_scale[layer]`` [num_tokens,
-num_kv_heads, 2] the K and V scale of each slot and head; ``store_kv``
-quantises (never deferred), ``dtype`` stays the model's (q/k/v) type.
+num_kv_heads, 2] the K and V scale of each slot and head; a store quantises
+(a deferred one inside the fp8 decode launch, with the same arithmetic),
+``dtype`` stays the model's (q/k/v) type.
 """
 
 from __future__ import annotations
@@ -70,11 +71,16 @@ class MHAKVCache:
 
     def store_kv(self, k: torch.Tensor, v: torch.Tensor, out_loc: torch.Tensor, layer_id: int) -> None:
         """kvcache/pool.py:47-50: write this step's k/v ([T, Hkv, D]) to slots out_loc ([T])."""
-        if self.quantized:
-            ops.store_kv_fp8(k, v, out_loc, self.k[layer_id], self.v[layer_id], self.kv_scale[layer_id])
-        elif self.defer_stores:
+        if self.defer_stores:
             self.flush(layer_id)
             self._pending[layer_id] = (k, v, out_loc)
+        else:
+            self.store_now(k, v, out_loc, layer_id)
+
+    def store_now(self, k: torch.Tensor, v: torch.Tensor, out_loc: torch.Tensor, layer_id: int) -> None:
+        """The store itself (quantising for fp8 pools), whatever ``defer_stores`` says."""
+        if self.quantized:
+            ops.store_kv_fp8(k, v, out_loc, self.k[layer_id], self.v[layer_id], self.kv_scale[layer_id])
         else:
             ops.store_kv(k, v, out_loc, self.k[layer_id], self.v[layer_id])
 
@@ -84,9 +90,10 @@ class MHAKVCache:
         """layers.py:107-109 fused: rotate q and k, store rotated k and raw v; returns rotated q.
 
         ``rotary`` carries ``inv_freq`` and ``dims`` (a ``layers.RotaryEmbedding``).
-        The store happens now, whatever ``defer_stores`` says."""
+        Unquantised pools: the store happens now, whatever ``defer_stores`` says.
+        fp8 pools: rotate, then the quantising store (deferred like ``store_kv``)."""
         self.flush(layer_id)
-        if self.quantized:  # rotate, then the quantising store
+        if self.quantized:
             q_rot = ops.rope(q, positions, rotary.inv_freq, rotary.dims, out=q_out)
             k_rot = ops.rope(k, positions, rotary.inv_freq, rotary.dims, out=k_out)
             self.store_kv(k_rot, v, out_loc, layer_id)
@@ -105,8 +112,7 @@ class MHAKVCache:
         for i in layers:
             pending = self.take_pending(i)
             if pending is not None:
-                k, v, out_loc = pending
-                ops.store_kv(k, v, out_loc, self.k[i], self.v[i])
+                self.store_now(*pending, i)
 
     @property
     def nbytes(self) -> int:

@@ -177,7 +177,8 @@ def paged_decode_attention(
 
     fp8 pools (``torch.float8_e4m3fn``, written by ``store_kv_fp8``) take
     ``kv_scale`` (float32 [N, Hkv, 2]: K scale, V scale); q is bf16/fp16 and the
-    result is the decode over the dequantised pool (no fused store).
+    result is the decode over the dequantised pool. With ``new_kv`` the launch
+    quantises and stores the new rows exactly as ``store_kv_fp8`` would.
 
     q [B, Hq, D]; pools [N, Hkv, D]; kv_indptr [B+1] int32; kv_indices int32
     (token slots, or page ids when page_size > 1 with seq_lens [B] given).
@@ -197,8 +198,8 @@ def paged_decode_attention(
         raise ValueError(f"head_dim mismatch or Hq ({hq}) not a multiple of Hkv ({hkv})")
     fp8 = k_pool.dtype == torch.float8_e4m3fn
     if fp8:
-        if v_pool.dtype != k_pool.dtype or kv_scale is None or new_kv is not None:
-            raise ValueError("fp8 pools need both pools fp8, kv_scale and no new_kv")
+        if v_pool.dtype != k_pool.dtype or kv_scale is None:
+            raise ValueError("fp8 pools need both pools fp8 and kv_scale")
         if q.dtype not in (torch.bfloat16, torch.float16):
             raise ValueError("fp8 pools take bf16 or fp16 queries")
         if kv_scale.dtype != torch.float32 or kv_scale.shape != (n_slots, hkv, 2):
@@ -237,7 +238,7 @@ def paged_decode_attention(
         b, hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
         max_splits, _lib.ptr(out), _lib.ptr(workspace), ws_bytes, _lib.current_stream(dev),
     )
-    if fp8:
+    if fp8 and new_kv is None:
         fn = lib.msgl_paged_decode_fp8_planned if planned else lib.msgl_paged_decode_fp8
         status = fn(_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool), _lib.ptr(kv_scale), *common)
         _lib.check(status, "msgl_paged_decode_fp8")
@@ -254,12 +255,20 @@ def paged_decode_attention(
         for name, t in (("k_new", k_new), ("v_new", v_new)):
             _check_device(name, t, dev)
         _check_index("out_loc", out_loc, dev)
-        fn = lib.msgl_paged_decode_store_planned if planned else lib.msgl_paged_decode_store
-        status = fn(
-            _lib.ptr(q), _lib.ptr(k_new), _lib.ptr(v_new), _lib.ptr(out_loc), _lib.ptr(k_pool), _lib.ptr(v_pool),
-            *common,
-        )
-        _lib.check(status, "msgl_paged_decode_store")
+        if fp8:
+            fn = lib.msgl_paged_decode_store_fp8_planned if planned else lib.msgl_paged_decode_store_fp8
+            status = fn(
+                _lib.ptr(q), _lib.ptr(k_new), _lib.ptr(v_new), _lib.ptr(out_loc), _lib.ptr(k_pool), _lib.ptr(v_pool),
+                _lib.ptr(kv_scale), *common,
+            )
+            _lib.check(status, "msgl_paged_decode_store_fp8")
+        else:
+            fn = lib.msgl_paged_decode_store_planned if planned else lib.msgl_paged_decode_store
+            status = fn(
+                _lib.ptr(q), _lib.ptr(k_new), _lib.ptr(v_new), _lib.ptr(out_loc), _lib.ptr(k_pool), _lib.ptr(v_pool),
+                *common,
+            )
+            _lib.check(status, "msgl_paged_decode_store")
     return out
 
 

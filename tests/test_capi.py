@@ -162,6 +162,14 @@ def test_host_side_argument_errors():
     assert df(hq=128) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()  # group 16
     assert df(d=96) == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
     assert df(sc=12) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
+    # fp8 decode with the fused store: (q, k_new, v_new, out_loc, kp, vp, kv_scale, indptr, ...)
+    dsf = lambda kn=16, loc=16, sc=16, dtype=1: lib.msgl_paged_decode_store_fp8(  # noqa: E731
+        16, kn, 16, loc, 16, 16, sc, 16, 16, nul, 4, 16, 8, 128, 1, 100, dtype, 0.1, 1, 16, 256, 1 << 30, nul)
+    assert dsf(sc=nul) == _lib.MSGL_ERR_INVALID and "kv_scale" in _lib.last_error()
+    assert dsf(kn=nul) == _lib.MSGL_ERR_INVALID and "k_new" in _lib.last_error()
+    assert dsf(loc=nul) == _lib.MSGL_ERR_INVALID and "out_loc" in _lib.last_error()
+    assert dsf(kn=24) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
+    assert dsf(dtype=0) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()
     # fp8 prefill: (q, kp, vp, kv_scale, q_indptr, kv_indptr, kv_indices, seq_lens, R, T, maxE, maxL, Hq, Hkv, D,
     #               page, slots, dtype, scale, splits, out, ws, ws_bytes, stream)
     pf8 = lambda dtype=1, sc=16, d=128: lib.msgl_prefill_ragged_fp8(  # noqa: E731

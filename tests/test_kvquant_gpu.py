@@ -136,6 +136,58 @@ def test_fp8_planned_matches_unplanned(cuda_device):
     assert torch.equal(a, b)
 
 
+@pytest.mark.parametrize("dt", ["bf16", "f16"])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256), (64, 8, 128)])
+@pytest.mark.parametrize("planned", [False, True])
+def test_fp8_fused_store_decode_bit_exact(cuda_device, dt, hq, hkv, d, planned):
+    """msgl_paged_decode_store_fp8 (the new token quantised and stored inside the
+    decode launch) against msgl_store_kv_fp8 followed by msgl_paged_decode_fp8:
+    output, codes and scales bit for bit, for single- and multi-chunk requests
+    and a request whose only token is the new one; a slot outside the pool is
+    skipped by both."""
+    dtype = DTYPES[dt]
+    lens = [1, 2, 17, 64, 65, 700, 2500]
+    n = 16384
+    c = workloads.decode_case_from_lens(lens, num_slots=n, seed=11)
+    b = len(lens)
+    q = randn((b, hq, d), 400, dtype).to(cuda_device)
+    g = torch.Generator(device=cuda_device).manual_seed(401)
+    k_new = (torch.randn((b, hkv, d), generator=g, device=cuda_device) *
+             torch.exp(torch.randn((b, hkv, 1), generator=g, device=cuda_device))).to(dtype)
+    v_new = (torch.randn((b, hkv, d), generator=g, device=cuda_device) *
+             torch.exp(torch.randn((b, hkv, 1), generator=g, device=cuda_device))).to(dtype)
+    k_new[3, 0] = 0  # a row of zeros: +0 codes, scale 0
+    out_loc = i32(c.out_loc, cuda_device)
+    ip, ix = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    for splits in (1, None, 16):
+        kp, vp, sc, _, _ = _fp8_pools(n, hkv, d, 402, cuda_device)
+        kp2, vp2, sc2 = kp.clone(), vp.clone(), sc.clone()
+        msplits = splits if splits is not None else ops.default_splits(b, hkv, max(lens))
+        ws = ops.decode_workspace(b, hq, hkv, d, msplits, cuda_device)
+        print(f"case fp8 fused store {hq}/{hkv}/{d} {dt} planned={planned} splits={splits}", flush=True)
+        ops.store_kv_fp8(k_new, v_new, out_loc, kp, vp, sc)
+        a = ops.paged_decode_attention(q, kp, vp, ip, ix, d**-0.5, max_splits=msplits, kv_scale=sc)
+        if planned:
+            ops.paged_decode_plan(ip, None, b, hq, hkv, d, msplits, ws)
+        f = ops.paged_decode_attention(q, kp2, vp2, ip, ix, d**-0.5, max_splits=msplits, kv_scale=sc2,
+                                       new_kv=(k_new, v_new, out_loc), workspace=ws, planned=planned)
+        torch.cuda.synchronize()
+        assert torch.equal(a, f), f"output splits={splits}"
+        assert torch.equal(kp.view(torch.uint8), kp2.view(torch.uint8)), "K codes"
+        assert torch.equal(vp.view(torch.uint8), vp2.view(torch.uint8)), "V codes"
+        assert torch.equal(sc, sc2), "scales"
+    # out_loc outside the pool: neither form writes anything
+    bad = out_loc.clone()
+    bad[2] = n + 5
+    kp, vp, sc, _, _ = _fp8_pools(n, hkv, d, 403, cuda_device)
+    before = (kp.view(torch.uint8).clone(), vp.view(torch.uint8).clone(), sc.clone())
+    ops.paged_decode_attention(q, kp, vp, ip, ix, d**-0.5, kv_scale=sc, new_kv=(k_new, v_new, bad))
+    torch.cuda.synchronize()
+    changed = (kp.view(torch.uint8) != before[0]).any(dim=(1, 2)).nonzero().flatten().tolist()
+    assert sorted(changed) == sorted(int(x) for i, x in enumerate(c.out_loc) if i != 2)
+    assert torch.equal(sc[n - 1], before[2][n - 1])
+
+
 def test_fp8_decode_headline_batch(cuda_device):
     """The headline decode shape (batch 128, L ~ U[200, 2048], 262144-slot pool) over an fp8 pool:
     sampled requests vs the oracle, and the quantisation error against the unquantised decode."""
