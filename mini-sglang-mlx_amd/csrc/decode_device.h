@@ -1,0 +1,545 @@
+// Device side of the paged decode (paged_decode.hip): parameters, the decode
+// and split-K merge bodies, shared with the single-launch mixed step
+// (mixed.hip). The design notes are at the top of paged_decode.hip.
+#pragma once
+#include <type_traits>
+
+#include "msgl_common.h"
+
+namespace msgl {
+namespace dec {
+
+#ifndef MSGL_DECODE_MIN_CHUNK
+#define MSGL_DECODE_MIN_CHUNK 64
+#endif
+constexpr int kMinChunk = MSGL_DECODE_MIN_CHUNK;  // smallest split-K chunk (tokens)
+constexpr int kMaxSplits = 64;  // bound on splits per request
+constexpr int kSeg = 512;       // token slots staged in LDS at a time
+constexpr int kSlotPad = 16 * 7;  // room for up to 7 padding tiles of prefetch
+constexpr float kLog2e = 1.4426950408889634f;
+
+// ---- per-dtype matrix-core step for S = Q K^T over one 16-byte chunk ------
+template <typename T>
+struct QK;
+
+template <>
+struct QK<bf16_t> {
+  static constexpr int VEC = 8;  // elements per 16-byte lane chunk
+  __device__ __forceinline__ static f32x4 step(const u32x4& a, const u32x4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c,
+                                                   0, 0, 0);
+  }
+};
+
+template <>
+struct QK<f16_t> {
+  static constexpr int VEC = 8;
+  __device__ __forceinline__ static f32x4 step(const u32x4& a, const u32x4& b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0,
+                                                  0, 0);
+  }
+};
+
+template <>
+struct QK<float> {
+  static constexpr int VEC = 4;
+  __device__ __forceinline__ static f32x4 step(const u32x4& a, const u32x4& b, f32x4 c) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      c = __builtin_amdgcn_mfma_f32_16x16x4f32(__uint_as_float(a[e]), __uint_as_float(b[e]), c, 0, 0, 0);
+    return c;
+  }
+};
+
+// fp8 K elements -> the 16-bit MFMA B operand of the query's type. Every e4m3
+// value is exactly representable in bf16 and fp16, so the products on the
+// matrix core are those of the dequantised row up to its per-row scale.
+template <typename T>
+__device__ __forceinline__ u32x4 fp8x8_to(uint32_t w0, uint32_t w1);
+template <>
+__device__ __forceinline__ u32x4 fp8x8_to<bf16_t>(uint32_t w0, uint32_t w1) {
+  typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+  return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w0, 1.0f, true)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w1, 1.0f, true))};
+}
+template <>
+__device__ __forceinline__ u32x4 fp8x8_to<f16_t>(uint32_t w0, uint32_t w1) {
+  return u32x4{__builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
+               __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
+}
+
+// Split geometry of one request: chunks of the batch-wide length chunk_len
+// (the plan kernel's ceil(max_b L_b / max_splits), a multiple of 16 tokens),
+// at most max_splits of them, the last one taking the rest. Used identically
+// by the plan, decode and merge kernels.
+__device__ __forceinline__ void split_geometry(int L, int max_splits, int chunk_len, int& n, int& chunk) {
+  if (L <= 0) {
+    n = 0;
+    chunk = 0;
+    return;
+  }
+  chunk = chunk_len;
+  n = min(max_splits, (L + chunk - 1) / chunk);
+}
+
+__device__ __forceinline__ int slot_of(const int32_t* __restrict__ kv_indices, int start, int tok, int page_size,
+                                       int64_t num_slots) {
+  int64_t s;
+  if (page_size == 1) {
+    s = kv_indices[start + tok];
+  } else {
+    s = (int64_t)kv_indices[start + tok / page_size] * page_size + tok % page_size;
+  }
+  return (s >= 0 && s < num_slots) ? (int)s : 0;
+}
+
+struct DecodeParams {
+  const void* q;
+  const void* k_pool;
+  const void* v_pool;
+  const float* kv_scale;  // fp8 pools: [num_slots, Hkv, 2] (K, V) scales per slot and kv head
+  float* kv_scale_w;      // the same, written by the fused store of an fp8 decode
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  const int32_t* seq_lens;
+  void* out;
+  float* part_ml;     // [B, S, Hq, 2]
+  float* part_o;      // [B, S, Hq, D]
+  // fused KV store (all null for plain decode): this step's rows [B, Hkv, D]
+  const void* k_new;
+  const void* v_new;
+  const int32_t* out_loc;  // [B] slot of each request's newest token (position L_b - 1)
+  void* k_pool_w;
+  void* v_pool_w;
+  // work list (plan kernel output, in the workspace)
+  int* meta;        // [0] items in the plan, [1] batch-wide chunk length
+  int4* plan;       // (request, split, kv-head group, 0), longest first
+  int64_t num_slots;
+  int hq, hkv, page_size, max_splits, batch, ngrp;
+  bool planned;  // the workspace already holds this call's plan
+  float scale_log2;
+};
+
+// LDS per wavefront: P tile [16 tokens][16 rows] + alpha[16] + (m, l)[16 rows].
+constexpr int kLdsPerWave = 16 * 16 + 16 + 32;
+
+// One 16-token tile of K and V rows as loaded: both in row layout (LPR
+// consecutive lanes read one whole row, R rows per instruction). KV is the
+// pool's storage type; an fp8 tile also carries the scales of the token this
+// lane's MFMA column holds.
+template <typename KV, int D>
+struct TileBuf {
+  static constexpr int VEC = 16 / (int)sizeof(KV);
+  static constexpr int NL = 16 / (64 / (D / VEC));
+  u32x4 k[NL];
+  u32x4 v[NL];
+  float ks, vs;
+};
+
+// Per-wave LDS K tile: 16 rows of D elements, row stride padded by 16 bytes so
+// row-wise writes and 16-row column reads are both free of bank conflicts.
+template <typename KV, int D>
+constexpr int k_lds_stride() { return D * (int)sizeof(KV) + 16; }
+
+// Minimum wavefronts per SIMD the register allocator must allow (occupancy).
+#ifndef MSGL_DECODE_MIN_WAVES
+#define MSGL_DECODE_MIN_WAVES 2
+#endif
+// Tiles of K/V held in registers per wavefront (1 computing + NST-1 in flight).
+#ifndef MSGL_DECODE_STAGES
+#define MSGL_DECODE_STAGES 2
+#endif
+#ifndef MSGL_DECODE_FP8_STAGES
+#define MSGL_DECODE_FP8_STAGES 2
+#endif
+
+// T: the query/output type; KV: the pool's storage type (T itself, or fp8e4m3
+// for a quantised pool with per-(slot, kv head) scales).
+template <typename T, typename KV, int D, int G>
+__device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg) {
+  constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
+  constexpr int VEC = QK<T>::VEC;   // query elements per 16-byte chunk (MFMA operand)
+  constexpr int ES = sizeof(T);
+  constexpr int VKV = 16 / (int)sizeof(KV);  // pool elements per 16-byte chunk
+  constexpr int EKV = sizeof(KV);
+  constexpr int KCHUNK = 4 * VEC;   // d covered by one MFMA step across the 4 row groups
+  constexpr int NLK = D / KCHUNK;   // MFMA steps per 16-token tile
+  constexpr int LPR = D / VKV;      // lanes per K/V row
+  constexpr int R = 64 / LPR;       // K/V rows per wave load
+  constexpr int NLV = 16 / R;       // K/V loads per lane per tile
+  constexpr int NR = G < 4 ? G : 4; // MFMA accumulator rows holding query heads
+  // register budget; fp8 tiles are half the bytes, so they keep more in flight
+  constexpr int NST = Q8 ? (G <= 2 && D <= 128 ? MSGL_DECODE_FP8_STAGES : 2)
+                         : ((sizeof(T) == 4 || D > 128 || G > 4) ? 2 : MSGL_DECODE_STAGES);
+  static_assert(NST >= 2 && (NST - 1) * 16 <= kSlotPad, "pipeline depth");
+  static_assert(D % KCHUNK == 0 && 64 % LPR == 0 && 16 % R == 0, "unsupported head_dim");
+  static_assert(G >= 1 && G <= 16, "unsupported group size");
+  static_assert(!Q8 || (sizeof(T) == 2 && G <= 8), "fp8 pools take 16-bit queries and groups up to 8");
+
+  extern __shared__ float lds_all[];
+  int* slots_lds = reinterpret_cast<int*>(lds_all);  // [kSeg + kSlotPad]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int nwaves = blockDim.x >> 6;
+  constexpr int KRS = k_lds_stride<KV, D>();
+  float* lds = lds_all + kSeg + kSlotPad + wave * (kLdsPerWave + 16 * KRS / 4);
+  float* P_lds = lds;              // [16][16]
+  float* A_lds = lds + 256;        // [16]
+  float* ML_lds = lds + 256 + 16;  // [16][2]
+  uint8_t* K_lds = reinterpret_cast<uint8_t*>(lds + kLdsPerWave);  // [16][KRS bytes]
+
+  // work item from the plan (workgroups past its end have nothing to do); a
+  // kv-head group is this workgroup's waves
+  if (wg >= p.meta[0]) return;
+  const int4 item = p.plan[wg];
+  const int b = item.x;
+  const int split = item.y;
+  const int kgrp = item.z;
+  const int start = p.kv_indptr[b];
+  const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - start;
+  int n, chunk;
+  split_geometry(L, p.max_splits, p.meta[1], n, chunk);
+  if (split >= n) {
+    if (split == 0) {  // L == 0: defined zero output for this group's heads
+      const int h0 = kgrp * nwaves * G;
+      const int h1 = min(p.hq, h0 + nwaves * G);
+      T* o = reinterpret_cast<T*>(p.out) + (int64_t)b * p.hq * D;
+      for (int i = h0 * D + threadIdx.x; i < h1 * D; i += blockDim.x) o[i] = from_f32<T>(0.f);
+    }
+    return;
+  }
+  const int t0 = split * chunk;
+  const int t1 = split == n - 1 ? L : t0 + chunk;
+
+  const int r = lane & 15;    // MFMA column (token in tile) / A row
+  const int g4 = lane >> 4;   // MFMA row group
+  const int vc = lane % LPR;  // V: 16-byte chunk within the row
+  const int vr = lane / LPR;  // V: token sub-row
+
+  const int64_t row_stride = (int64_t)p.hkv * D * EKV;  // bytes per slot
+
+  {
+    const int kvh = kgrp * nwaves + wave;
+    const bool active = kvh < p.hkv;
+    const int kvh_c = active ? kvh : 0;
+
+    // Q fragment: A operand, row r = query head kvh*G + r (zero when r >= G).
+    u32x4 qa[NLK];
+    {
+      const uint8_t* qrow =
+          reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)b * p.hq + kvh_c * G + r) * D * ES + g4 * VEC * ES;
+#pragma unroll
+      for (int j = 0; j < NLK; ++j) {
+        qa[j] = (r < G) ? ld16(qrow + j * KCHUNK * ES) : u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+    float m_run[NR], l_run[NR];
+#pragma unroll
+    for (int i = 0; i < NR; ++i) {
+      m_run[i] = -INFINITY;
+      l_run[i] = 0.f;
+    }
+    float acc[G][VKV];
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+      for (int e = 0; e < VKV; ++e) acc[g][e] = 0.f;
+
+    const uint8_t* kbase_p = reinterpret_cast<const uint8_t*>(p.k_pool) + (int64_t)kvh_c * D * EKV + vc * 16;
+    const uint8_t* vbase_p = reinterpret_cast<const uint8_t*>(p.v_pool) + (int64_t)kvh_c * D * EKV + vc * 16;
+
+    // Fused KV store (unquantised pools): the chunk holding position L-1 (the
+    // new token) writes its rows to the pool and reads them from k_new/v_new
+    // instead -- no other unit reads that slot, so the write needs no ordering
+    // inside the launch.
+    const bool fused = !Q8 && p.k_new != nullptr;
+    const int new_pos = fused && t1 == L ? L - 1 : 0x7fffffff;  // absolute position, or never
+    const int64_t new_off = ((int64_t)b * p.hkv + kvh_c) * D * ES + vc * VEC * ES;
+    const uint8_t* knew_p = fused ? reinterpret_cast<const uint8_t*>(p.k_new) + new_off : nullptr;
+    const uint8_t* vnew_p = fused ? reinterpret_cast<const uint8_t*>(p.v_new) + new_off : nullptr;
+    if (active && new_pos != 0x7fffffff && lane < LPR) {
+      const int64_t slot = p.out_loc[b];
+      if (slot >= 0 && slot < p.num_slots) {
+        const int64_t dst = slot * row_stride + (int64_t)kvh * D * ES + vc * VEC * ES;
+        st16(reinterpret_cast<uint8_t*>(p.k_pool_w) + dst, ld16(knew_p));
+        st16(reinterpret_cast<uint8_t*>(p.v_pool_w) + dst, ld16(vnew_p));
+      }
+    }
+    // Fused store over fp8 pools: the chunk holding the new token quantises its
+    // K and V rows exactly like msgl_store_kv_fp8 (lanes [0, LQ) the K row,
+    // [LQ, 2 LQ) the V row, one 16-byte chunk of T each) and writes codes and
+    // scales before any load of the chunk is issued; the loop then reads the
+    // new token from the pool like every other token.
+    if constexpr (Q8) {
+      if (active && p.k_new != nullptr && t1 == L) {
+        constexpr int LQ = D / VEC;  // lanes per input row
+        static_assert(2 * LQ <= 64, "a wavefront quantises the K and V rows together");
+        const int sub = lane % LQ;
+        const bool is_v = (lane / LQ) & 1;  // lanes >= 2 LQ repeat the rows and write nothing
+        const uint8_t* src = reinterpret_cast<const uint8_t*>(is_v ? p.v_new : p.k_new) +
+                             (((int64_t)b * p.hkv + kvh) * D + sub * VEC) * ES;
+        uint32_t w[VEC / 4];
+        const float amax = fp8_quantize_chunk<T>(ld16(src), LQ, w);
+        const int64_t slot = p.out_loc[b];
+        if (lane < 2 * LQ && slot >= 0 && slot < p.num_slots) {
+          uint8_t* dst = reinterpret_cast<uint8_t*>(is_v ? p.v_pool_w : p.k_pool_w) +
+                         (slot * p.hkv + kvh) * D + sub * VEC;
+          static_assert(VEC == 8, "16-bit queries: eight codes per lane");
+          *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
+          if (sub == 0) p.kv_scale_w[(slot * p.hkv + kvh) * 2 + (is_v ? 1 : 0)] = amax / 448.f;
+        }
+        // the stores have completed before this wavefront loads the slot back
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+      }
+    }
+
+    for (int s0 = t0; s0 < t1; s0 += kSeg) {
+      const int seg_len = min(kSeg, t1 - s0);
+      const int ntile = (seg_len + 15) >> 4;
+      // ---- stage this segment's slots, padded by NST-1 tiles; positions past
+      //      the end repeat the last valid slot ----
+      __syncthreads();
+      for (int i = threadIdx.x; i < (ntile + NST - 1) * 16; i += blockDim.x) {
+        const int tok = s0 + min(i, seg_len - 1);
+        slots_lds[i] = slot_of(p.kv_indices, start, tok, p.page_size, p.num_slots);
+      }
+      __syncthreads();
+      if (!active) continue;
+
+      // Prefetches past the segment end read the padded slot list (the last
+      // valid slot, one row per tile, already fetched): every path through the
+      // loop keeps the same loads in flight, so the compiler waits for exactly
+      // one tile instead of draining the pipeline at each branch.
+      auto issue = [&](TileBuf<KV, D>& buf, int tile) {
+        const int base = tile * 16;
+#pragma unroll
+        for (int i = 0; i < NLV; ++i) {
+          const int pos = base + vr + R * i;
+          const int64_t off = (int64_t)slots_lds[pos] * row_stride;
+          const bool is_new = s0 + pos >= new_pos;  // the new token and the padding that repeats it
+          buf.k[i] = ld16_stream(is_new ? knew_p : kbase_p + off);
+          buf.v[i] = ld16_stream(is_new ? vnew_p : vbase_p + off);
+        }
+        if (Q8) {  // the K and V scales of the token in this lane's MFMA column: one 8-byte load
+          const float2 sc = reinterpret_cast<const float2*>(p.kv_scale)[(int64_t)slots_lds[base + r] * p.hkv + kvh_c];
+          buf.ks = sc.x;
+          buf.vs = sc.y;
+        }
+      };
+
+      auto compute = [&](const TileBuf<KV, D>& buf, int tile) {
+        // K rows -> LDS -> MFMA B layout (lane: token r, d chunk j*KCHUNK + g4*VEC)
+        wave_lds_sync();
+#pragma unroll
+        for (int i = 0; i < NLV; ++i) *reinterpret_cast<u32x4*>(K_lds + (vr + R * i) * KRS + vc * 16) = buf.k[i];
+        wave_lds_sync();
+        // S = Q K^T on the matrix core
+        f32x4 s = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int j = 0; j < NLK; ++j) {
+          if constexpr (Q8) {
+            const uint2 k8 = *reinterpret_cast<const uint2*>(K_lds + r * KRS + (j * KCHUNK + g4 * VEC));
+            s = QK<T>::step(qa[j], fp8x8_to<T>(k8.x, k8.y), s);
+          } else {
+            s = QK<T>::step(qa[j], *reinterpret_cast<const u32x4*>(K_lds + r * KRS + (j * KCHUNK + g4 * VEC) * ES),
+                            s);
+          }
+        }
+        // online softmax (exp2 domain); a quantised row's scale multiplies its scores
+        const float sc = Q8 ? p.scale_log2 * buf.ks : p.scale_log2;
+        const bool valid = tile * 16 + r < seg_len;
+        float pr[4] = {0.f, 0.f, 0.f, 0.f}, al[4] = {1.f, 1.f, 1.f, 1.f};
+#pragma unroll
+        for (int i = 0; i < NR; ++i) {
+          const float x = valid ? s[i] * sc : -INFINITY;
+          const float mt = row16_max(x);
+          const float m_new = fmaxf(m_run[i], mt);
+          al[i] = __builtin_amdgcn_exp2f(m_run[i] - m_new);
+          pr[i] = __builtin_amdgcn_exp2f(x - m_new);
+          l_run[i] = l_run[i] * al[i] + pr[i];
+          m_run[i] = m_new;
+        }
+        wave_lds_sync();  // previous tile's LDS reads are done
+        // P V weights; a quantised V row's scale is folded into its weight (l keeps the plain weights)
+        const float vsc = Q8 ? buf.vs : 1.f;
+        *reinterpret_cast<f32x4*>(P_lds + r * 16 + 4 * g4) = f32x4{pr[0] * vsc, pr[1] * vsc, pr[2] * vsc, pr[3] * vsc};
+        if (r == 0) *reinterpret_cast<f32x4*>(A_lds + 4 * g4) = f32x4{al[0], al[1], al[2], al[3]};
+        wave_lds_sync();
+        // O = alpha * O + P V on the VALU
+        float alpha[G];
+#pragma unroll
+        for (int g = 0; g < G; ++g) alpha[g] = A_lds[g];
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < VKV; ++e) acc[g][e] *= alpha[g];
+#pragma unroll
+        for (int i = 0; i < NLV; ++i) {
+          const int tl = vr + R * i;
+          float vf[VKV];
+          Vec16<KV>::to_f32(buf.v[i], vf);
+          float pv[G];
+#pragma unroll
+          for (int g = 0; g < G; ++g) pv[g] = P_lds[tl * 16 + g];
+#pragma unroll
+          for (int g = 0; g < G; ++g)
+#pragma unroll
+            for (int e = 0; e < VKV; ++e) acc[g][e] = fmaf(pv[g], vf[e], acc[g][e]);
+        }
+      };
+
+      // NST-stage register pipeline: tiles t+1 .. t+NST-1 are in flight while t computes
+      TileBuf<KV, D> buf[NST];
+#pragma unroll
+      for (int i = 0; i < NST - 1; ++i) issue(buf[i], i);  // tiles past ntile are padding
+      for (int tile = 0; tile < ntile; tile += NST) {
+#pragma unroll
+        for (int k = 0; k < NST; ++k) {
+          const int t = tile + k;
+          if (t >= ntile) break;
+          issue(buf[(k + NST - 1) % NST], t + NST - 1);
+          compute(buf[k], t);
+        }
+      }
+    }
+    if (!active) return;
+
+    // ---- fold: l over the 16 token lanes, acc over the R token sub-rows ----
+#pragma unroll
+    for (int i = 0; i < NR; ++i) l_run[i] = row16_sum(l_run[i]);
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1)
+#pragma unroll
+      for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int e = 0; e < VKV; ++e) acc[g][e] += __shfl_xor(acc[g][e], off);
+    wave_lds_sync();
+    if (r == 0) {
+#pragma unroll
+      for (int i = 0; i < NR; ++i) {
+        ML_lds[(4 * g4 + i) * 2 + 0] = m_run[i];
+        ML_lds[(4 * g4 + i) * 2 + 1] = l_run[i];
+      }
+    }
+    wave_lds_sync();
+    const int d0 = vc * VKV;
+    if (n == 1) {
+      if (lane < LPR) {
+        T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D + d0;
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+          const float inv = 1.f / ML_lds[g * 2 + 1];
+#pragma unroll
+          for (int c = 0; c < VKV; c += VEC) {
+            T tmp[VEC];
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) tmp[e] = from_f32<T>(acc[g][c + e] * inv);
+            u32x4 packed;
+            __builtin_memcpy(&packed, tmp, 16);
+            st16(o + g * D + c, packed);
+          }
+        }
+      }
+      return;
+    }
+
+    // ---- split-K: publish this chunk's partials for the merge kernel ----
+    const int64_t base = ((int64_t)b * p.max_splits + split) * p.hq + kvh * G;
+    if (lane < LPR) {
+#pragma unroll
+      for (int g = 0; g < G; ++g) {
+        float* po = p.part_o + (base + g) * D + d0;
+#pragma unroll
+        for (int e = 0; e < VKV; e += 4)
+          *reinterpret_cast<f32x4*>(po + e) = f32x4{acc[g][e], acc[g][e + 1], acc[g][e + 2], acc[g][e + 3]};
+      }
+    }
+    if (lane < G) {
+      p.part_ml[(base + lane) * 2 + 0] = ML_lds[lane * 2 + 0];
+      p.part_ml[(base + lane) * 2 + 1] = ML_lds[lane * 2 + 1];
+    }
+  }
+}
+
+// Merge split-K partials, one wavefront per (request, kv head):
+//   o = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s
+// (the combine of the Metal kernel's simdgroup merge, attention/metal.py:75-94).
+// Lanes own float4 chunks of the G*D outputs; the partials of up to 8 splits
+// are loaded in one batch (one memory round trip) and combined online.
+template <typename T, int D, int G>
+__device__ __forceinline__ void paged_decode_merge_body(const DecodeParams& p, int batch, int wg) {
+  const int unit = wg * (blockDim.x >> 6) + (threadIdx.x >> 6);  // (b, kvh)
+  const int lane = threadIdx.x & 63;
+  if (unit >= batch * p.hkv) return;
+  const int b = unit / p.hkv, kvh = unit % p.hkv;
+  const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];
+  int n, chunk;
+  split_geometry(L, p.max_splits, p.meta[1], n, chunk);
+  if (n <= 1) return;
+  const int64_t bbase = (int64_t)b * p.max_splits * p.hq + kvh * G;
+  constexpr int C4 = D / 4;
+  constexpr int NB = 8;  // splits whose partials are loaded in one batch
+  T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D;
+  for (int c = lane; c < G * C4; c += 64) {
+    const int g = c / C4, d4 = c % C4;
+    const float2* ml = reinterpret_cast<const float2*>(p.part_ml) + bbase + g;
+    const float* po = p.part_o + (bbase + g) * D + d4 * 4;
+    const int64_t mstride = p.hq;  // float2 units
+    const int64_t ostride = (int64_t)p.hq * D;
+    float M = -INFINITY, Lsum = 0.f;
+    f32x4 a = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < n; s0 += NB) {
+      // issue every load of this batch before using any of them
+      float2 mlv[NB];
+      f32x4 xv[NB];
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const int sp = min(s0 + i, n - 1);
+        mlv[i] = ml[sp * mstride];
+        xv[i] = *reinterpret_cast<const f32x4*>(po + sp * ostride);
+      }
+      float Mb = M;
+#pragma unroll
+      for (int i = 0; i < NB; ++i)
+        if (s0 + i < n) Mb = fmaxf(Mb, mlv[i].x);
+      const float r = __builtin_amdgcn_exp2f(M - Mb);  // rescale what was combined so far
+      Lsum *= r;
+      a *= r;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        if (s0 + i < n) {
+          const float f = __builtin_amdgcn_exp2f(mlv[i].x - Mb);
+          Lsum += f * mlv[i].y;
+          a += f * xv[i];
+        }
+      }
+      M = Mb;
+    }
+    const float inv = 1.f / Lsum;
+    T tmp[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) tmp[e] = from_f32<T>(a[e] * inv);
+    T* dst = o + g * D + d4 * 4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) dst[e] = tmp[e];
+  }
+}
+
+// Wavefronts per workgroup of the decode kernel (kv heads handled by one
+// workgroup). Small workgroups let a CU start new work as soon as any wave finishes.
+#ifndef MSGL_DECODE_WAVES_PER_WG
+#define MSGL_DECODE_WAVES_PER_WG 4
+#endif
+
+// Dynamic LDS of a decode workgroup of nwaves wavefronts.
+template <typename KV, int D>
+inline size_t decode_lds_bytes(int nwaves) {
+  return ((size_t)kSeg + kSlotPad + (size_t)nwaves * (kLdsPerWave + 16 * k_lds_stride<KV, D>() / 4)) * sizeof(float);
+}
+
+}  // namespace dec
+}  // namespace msgl
