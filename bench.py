@@ -60,6 +60,8 @@ def parse_args():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
+    ap.add_argument("--mixed-mode", default="single", choices=["single", "streams", "serial"],
+                    help="mixed step: one launch for decode + prefill, two streams, or one after the other")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--copy-calibration", action="store_true",
@@ -623,7 +625,8 @@ def bench_mixed(args, dev):
     def run(i, ev):
         if ev:
             ev[0].record()
-        step.run(q, kn, vn, kp, vp, out, d**-0.5)
+        step.run(q, kn, vn, kp, vp, out, d**-0.5, concurrent=args.mixed_mode == "streams",
+                 single_launch=args.mixed_mode == "single")
         if ev:
             ev[1].record()
 
@@ -634,11 +637,13 @@ def bench_mixed(args, dev):
         sec * 1e6, "us", sec * 1e3,
         "one step, Qwen3-8B attention (32 q / 8 kv heads, head_dim 128), one layer, page_size 16, 8M-slot bf16 "
         "pool: 128 decode requests (context U[512,32768], seed 0) + 2 prefill chunks of 1024 over prefixes "
-        "0 and 8192; indices built on the GPU from a req_to_token table; the prefill on a second stream "
-        "concurrent with the decode",
+        "0 and 8192; indices built on the GPU from a req_to_token table; decode and prefill "
+        + {"single": "in one launch (msgl_mixed_attention)", "streams": "on two concurrent streams",
+           "serial": "one after the other"}[args.mixed_mode],
         {"decode_requests": nd, "decode_sum_context": int(dec_lens.sum()), "prefill_tokens": int(ext.sum()),
          "decode_bytes": dec_bytes, "prefill_flops": pf_flops, "prefill_bytes": pf_bytes,
          "store_bytes": store_bytes, "decode_splits": step.decode_splits, "prefill_splits": step.prefill_splits,
+         "mode": args.mixed_mode,
          "step_gbs": round(nbytes / sec / 1e9, 2)},
         {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(ach / HBM_PEAK_GBS, 4),

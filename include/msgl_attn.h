@@ -26,6 +26,9 @@
  *   msgl_paged_decode_fp8,   decode over pools of e4m3 codes with one scale per slot and kv head,
  *   msgl_paged_decode_store_fp8  the two in one launch,
  *   msgl_prefill_ragged_fp8  and the ragged prefill over them)
+ *   msgl_mixed_attention     a batch's decode requests (attention/metal.py:112-131 + the store of
+ *                            kvcache/pool.py:47-50) and prefill chunks (attention/base.py:85-105)
+ *                            in one launch
  *
  * Layouts (identical to the reference, no transposes at the boundary):
  *   q, out   [T, Hq, D]   row-major, dtype `dtype`
@@ -369,6 +372,32 @@ int msgl_prefill_ragged_fp8_planned(const void* q, const void* k_pool, const voi
                                     int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
                                     int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
                                     int64_t workspace_bytes, void* stream);
+
+/*
+ * Mixed step in one launch: the paged decode of num_decode requests (one new
+ * token each; with k_new/v_new/out_loc the new token's KV store fused in, as in
+ * msgl_paged_decode_store) and the ragged prefill of num_prefill chunks, run
+ * by one grid whose workgroups take decode and prefill work items in
+ * proportion, then one merge launch for both split-K parts. The reference
+ * dispatches a whole batch to one phase (attention/base.py:49-60); per request
+ * the results are bit-identical to msgl_paged_decode_store_planned /
+ * msgl_prefill_ragged_planned with the same arguments, whose work lists
+ * msgl_paged_decode_plan (into dec_workspace) and msgl_prefill_plan (into
+ * pf_workspace) must have built for these indices and sizes. Both parts share
+ * the pools, head counts, head_dim (64 or 128), page size, dtype (bf16/fp16)
+ * and scale; q_dec/out_dec are [num_decode, Hq, D], q_pf/out_pf the packed
+ * [num_tokens, Hq, D] the prefill's q_indptr indexes (they may be views of one
+ * packed batch). With no request of one phase it runs the other's planned call.
+ */
+int msgl_mixed_attention(const void* q_dec, const void* k_new, const void* v_new, const int32_t* out_loc,
+                         const int32_t* dec_kv_indptr, const int32_t* dec_kv_indices, const int32_t* dec_seq_lens,
+                         int32_t num_decode, int32_t dec_max_splits, void* out_dec, void* dec_workspace,
+                         int64_t dec_workspace_bytes, const void* q_pf, const int32_t* q_indptr,
+                         const int32_t* pf_kv_indptr, const int32_t* pf_kv_indices, const int32_t* pf_seq_lens,
+                         int32_t num_prefill, int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                         int32_t pf_max_splits, void* out_pf, void* pf_workspace, int64_t pf_workspace_bytes,
+                         void* k_pool, void* v_pool, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                         int32_t page_size, int64_t num_slots, int32_t dtype, float scale, void* stream);
 
 #ifdef __cplusplus
 }

@@ -541,5 +541,14 @@ inline size_t decode_lds_bytes(int nwaves) {
   return ((size_t)kSeg + kSlotPad + (size_t)nwaves * (kLdsPerWave + 16 * k_lds_stride<KV, D>() / 4)) * sizeof(float);
 }
 
+// Validates the arguments of a decode call and fills p (workspace regions
+// included); empty: batch 0, nothing to launch. (paged_decode.hip)
+int decode_params(const char* fn, bool planned, const void* q, const void* k_new, const void* v_new,
+                  const int32_t* out_loc, const void* k_pool, const void* v_pool, const float* kv_scale,
+                  const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                  int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                  int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
+                  DecodeParams& p, bool& empty);
+
 }  // namespace dec
 }  // namespace msgl

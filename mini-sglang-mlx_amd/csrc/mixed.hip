@@ -1,0 +1,202 @@
+// Single-launch mixed step: the paged decode of a batch's decode requests and
+// the ragged prefill of its prefill chunks as one grid, then one merge launch.
+//
+// The reference dispatches a whole batch to one phase (attention/base.py:49-60,
+// core.py:111-116); per request the results here are exactly those of the
+// decode path (attention/naive.py:50-60 / attention/metal.py:112-131, with the
+// new token's store of kvcache/pool.py:47-50 fused in) or of the prefill path
+// (attention/base.py:85-105): each workgroup runs the unchanged decode or
+// prefill body on one work item of the lists msgl_paged_decode_plan and
+// msgl_prefill_plan built.
+//
+// Workgroup i takes prefill item floor(i nP / (nP + nD)) when that count steps
+// up at i, otherwise decode item i - floor(i nP / (nP + nD)) (nP, nD: the list
+// lengths the plans left in the workspaces): the two longest-first lists
+// interleave in proportion, so CUs hold HBM-bound decode and matrix-core-bound
+// prefill workgroups side by side from the first wave of dispatch on. Both
+// bodies run as 4-wavefront workgroups; the launch takes the larger LDS of the
+// two (the prefill ring) and the prefill's register budget.
+#include "decode_device.h"
+#include "prefill_device.h"
+
+namespace msgl {
+namespace {
+
+template <typename T, int D, int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf::G16<D>::WAVES))) void mixed_attention_kernel(
+    pf::PrefillParams pp, dec::DecodeParams dp) {
+  const int np = *pp.plan_count;
+  const int nd = dp.meta[0];
+  const int i = blockIdx.x;
+  if (i >= np + nd) return;
+  const int64_t tot = (int64_t)np + nd;
+  const int a = (int)((int64_t)i * np / tot);
+  const int a1 = (int)((int64_t)(i + 1) * np / tot);
+  if (a1 > a) {
+    pf::prefill16_body<T, T, D, G>(pp, a);
+  } else {
+    dec::paged_decode_body<T, T, D, G>(dp, i - a);
+  }
+}
+
+// The split-K merges of both parts: the first npm workgroups are the prefill
+// merge's (token tk = i % ntok, head block i / ntok), the rest the decode merge's.
+template <typename T, int D, int G>
+__global__ __launch_bounds__(256) void mixed_merge_kernel(pf::PrefillParams pp, dec::DecodeParams dp, int batch,
+                                                          int ntok, int npm) {
+  const int i = blockIdx.x;
+  if (i < npm) {
+    pf::prefill_merge_body<T, D>(pp, i % ntok, i / ntok);
+  } else {
+    dec::paged_decode_merge_body<T, D, G>(dp, batch, i - npm);
+  }
+}
+
+template <typename T, int D, int G>
+int launch_mixed(pf::PrefillParams pp, const dec::DecodeParams& dp, int batch, int max_e, hipStream_t stream) {
+  using Geo = pf::G16<D, (int)sizeof(T)>;
+  constexpr int BQ = Geo::ROWS / G;
+  static_assert(pf::THREADS16 == 256 && Geo::ROWS % G == 0, "both bodies run as 4-wavefront workgroups");
+  pp.nqb = (max_e + BQ - 1) / BQ;
+  const int64_t items_pf = (int64_t)pp.hkv * pp.num_reqs * pp.splits * pp.nqb;
+  if (items_pf > (int64_t)pp.plan_capacity) {
+    set_error("msgl_mixed_attention: prefill workspace holds %d work items, %lld needed", pp.plan_capacity,
+              (long long)items_pf);
+    return MSGL_ERR_WORKSPACE;
+  }
+  pp.items = (int)items_pf;
+  const int64_t items_dec = (int64_t)batch * dp.max_splits * dp.ngrp;
+  const size_t lds = std::max<size_t>(Geo::LDS_BYTES, dec::decode_lds_bytes<T, D>(4));
+  static bool attr_set = false;  // per process; the attribute is per function
+  if (lds > 65536 && !attr_set) {
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mixed_attention_kernel<T, D, G>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
+      set_error("msgl_mixed_attention: cannot raise the LDS limit to %zu bytes", lds);
+      return MSGL_ERR_HIP;
+    }
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((mixed_attention_kernel<T, D, G>), dim3((unsigned)(items_pf + items_dec)), dim3(256), lds,
+                     stream, pp, dp);
+  MSGL_CHECK_LAUNCH("msgl_mixed_attention");
+  constexpr int HPB = 256 / (D / 4);  // heads per prefill-merge workgroup
+  const int npm = pp.splits > 1 ? pp.num_tokens * ((pp.hq + HPB - 1) / HPB) : 0;
+  const int ndm = dp.max_splits > 1 ? (batch * dp.hkv + 3) / 4 : 0;
+  if (npm + ndm > 0) {
+    hipLaunchKernelGGL((mixed_merge_kernel<T, D, G>), dim3(npm + ndm), dim3(256), 0, stream, pp, dp, batch,
+                       pp.num_tokens, npm);
+    MSGL_CHECK_LAUNCH("msgl_mixed_attention (merge)");
+  }
+  return MSGL_OK;
+}
+
+template <typename T, int D>
+int mixed_group(const pf::PrefillParams& pp, const dec::DecodeParams& dp, int batch, int max_e, int group,
+                hipStream_t s) {
+  switch (group) {
+    case 1: return launch_mixed<T, D, 1>(pp, dp, batch, max_e, s);
+    case 2: return launch_mixed<T, D, 2>(pp, dp, batch, max_e, s);
+    case 4: return launch_mixed<T, D, 4>(pp, dp, batch, max_e, s);
+    case 8: return launch_mixed<T, D, 8>(pp, dp, batch, max_e, s);
+    default:
+      set_error("msgl_mixed_attention: Hq/Hkv = %d not built (1, 2, 4, 8)", group);
+      return MSGL_ERR_UNSUPPORTED;
+  }
+}
+
+template <typename T>
+int mixed_dim(const pf::PrefillParams& pp, const dec::DecodeParams& dp, int batch, int max_e, int head_dim, int group,
+              hipStream_t s) {
+  switch (head_dim) {
+    case 64: return mixed_group<T, 64>(pp, dp, batch, max_e, group, s);
+    case 128: return mixed_group<T, 128>(pp, dp, batch, max_e, group, s);
+    default:
+      set_error("msgl_mixed_attention: head_dim %d not built (64, 128)", head_dim);
+      return MSGL_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace
+}  // namespace msgl
+
+extern "C" int msgl_paged_decode_planned(const void* q, const void* k_pool, const void* v_pool,
+                                         const int32_t* kv_indptr, const int32_t* kv_indices,
+                                         const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                         int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                                         int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                                         int64_t workspace_bytes, void* stream);
+extern "C" int msgl_paged_decode_store_planned(const void* q, const void* k_new, const void* v_new,
+                                               const int32_t* out_loc, void* k_pool, void* v_pool,
+                                               const int32_t* kv_indptr, const int32_t* kv_indices,
+                                               const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                               int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                               int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                                               void* out, void* workspace, int64_t workspace_bytes, void* stream);
+extern "C" int msgl_prefill_ragged_planned(const void* q, const void* k_pool, const void* v_pool,
+                                           const int32_t* q_indptr, const int32_t* kv_indptr,
+                                           const int32_t* kv_indices, const int32_t* seq_lens, int32_t num_reqs,
+                                           int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                                           int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                                           int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                                           int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
+                                           void* stream);
+
+extern "C" int msgl_mixed_attention(const void* q_dec, const void* k_new, const void* v_new, const int32_t* out_loc,
+                                    const int32_t* dec_kv_indptr, const int32_t* dec_kv_indices,
+                                    const int32_t* dec_seq_lens, int32_t num_decode, int32_t dec_max_splits,
+                                    void* out_dec, void* dec_workspace, int64_t dec_workspace_bytes,
+                                    const void* q_pf, const int32_t* q_indptr, const int32_t* pf_kv_indptr,
+                                    const int32_t* pf_kv_indices, const int32_t* pf_seq_lens, int32_t num_prefill,
+                                    int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len,
+                                    int32_t pf_max_splits, void* out_pf, void* pf_workspace,
+                                    int64_t pf_workspace_bytes, void* k_pool, void* v_pool, int32_t num_qo_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                                    int32_t dtype, float scale, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(num_decode >= 0 && num_prefill >= 0, "msgl_mixed_attention: request counts must be >= 0");
+  if (num_decode == 0 || num_prefill == 0 || max_extend_len == 0 || num_tokens == 0) {  // one phase only
+    int st = MSGL_OK;
+    if (num_prefill > 0)
+      st = msgl_prefill_ragged_planned(q_pf, k_pool, v_pool, q_indptr, pf_kv_indptr, pf_kv_indices, pf_seq_lens,
+                                       num_prefill, num_tokens, max_extend_len, max_seq_len, num_qo_heads,
+                                       num_kv_heads, head_dim, page_size, num_slots, dtype, scale, pf_max_splits,
+                                       out_pf, pf_workspace, pf_workspace_bytes, stream);
+    if (st == MSGL_OK && num_decode > 0)
+      st = k_new != nullptr
+               ? msgl_paged_decode_store_planned(q_dec, k_new, v_new, out_loc, k_pool, v_pool, dec_kv_indptr,
+                                                 dec_kv_indices, dec_seq_lens, num_decode, num_qo_heads, num_kv_heads,
+                                                 head_dim, page_size, num_slots, dtype, scale, dec_max_splits,
+                                                 out_dec, dec_workspace, dec_workspace_bytes, stream)
+               : msgl_paged_decode_planned(q_dec, k_pool, v_pool, dec_kv_indptr, dec_kv_indices, dec_seq_lens,
+                                           num_decode, num_qo_heads, num_kv_heads, head_dim, page_size, num_slots,
+                                           dtype, scale, dec_max_splits, out_dec, dec_workspace, dec_workspace_bytes,
+                                           stream);
+    return st;
+  }
+  if (dtype != MSGL_BF16 && dtype != MSGL_F16) {
+    set_error("msgl_mixed_attention: bf16 or fp16 only (dtype %d)", dtype);
+    return MSGL_ERR_UNSUPPORTED;
+  }
+  MSGL_CHECK_ARG((k_new == nullptr) == (v_new == nullptr) && (k_new == nullptr || out_loc != nullptr),
+                 "msgl_mixed_attention: k_new, v_new and out_loc go together");
+  MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
+                 "msgl_mixed_attention: k_new and v_new must be 16-byte aligned");
+  pf::PrefillParams pp;
+  bool empty = false;
+  int st = pf::prefill_params("msgl_mixed_attention", pf::kRunPlanned, q_pf, k_pool, v_pool, nullptr, q_indptr,
+                              pf_kv_indptr, pf_kv_indices, pf_seq_lens, num_prefill, num_tokens, max_extend_len,
+                              max_seq_len, num_qo_heads, num_kv_heads, head_dim, page_size, num_slots, dtype, scale,
+                              pf_max_splits, out_pf, pf_workspace, pf_workspace_bytes, pp, empty);
+  if (st != MSGL_OK) return st;
+  dec::DecodeParams dp;
+  st = dec::decode_params("msgl_mixed_attention", true, q_dec, k_new, v_new, out_loc, k_pool, v_pool, nullptr,
+                          dec_kv_indptr, dec_kv_indices, dec_seq_lens, num_decode, num_qo_heads, num_kv_heads,
+                          head_dim, page_size, num_slots, dtype, scale, dec_max_splits, out_dec, dec_workspace,
+                          dec_workspace_bytes, dp, empty);
+  if (st != MSGL_OK) return st;
+  const int group = num_qo_heads / num_kv_heads;
+  hipStream_t s = (hipStream_t)stream;
+  return dtype == MSGL_BF16 ? mixed_dim<bf16_t>(pp, dp, num_decode, max_extend_len, head_dim, group, s)
+                            : mixed_dim<f16_t>(pp, dp, num_decode, max_extend_len, head_dim, group, s);
+}

@@ -404,17 +404,21 @@ extern "C" int msgl_paged_decode_store_fp8_planned(const void* q, const void* k_
                            stream);
 }
 
-static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, const void* k_new, const void* v_new,
+// Validates the arguments of a decode call and fills p (workspace regions
+// included); empty: batch 0, nothing to launch.
+int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const void* k_new, const void* v_new,
                              const int32_t* out_loc, const void* k_pool, const void* v_pool, const float* kv_scale,
-                             const int32_t* kv_indptr, const int32_t* kv_indices,
-                             const int32_t* seq_lens,
+                             const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
                              int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                              int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
-                             void* out, void* workspace, int64_t workspace_bytes, void* stream) {
-  using namespace msgl;
+                             void* out, void* workspace, int64_t workspace_bytes, DecodeParams& p, bool& empty) {
   clear_error();
+  empty = false;
   MSGL_CHECK_ARG(batch >= 0 && batch <= 65535, "%s: batch must be in [0, 65535]", fn);
-  if (batch == 0) return MSGL_OK;
+  if (batch == 0) {
+    empty = true;
+    return MSGL_OK;
+  }
   MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "%s: sizes must be > 0", fn);
   MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "%s: Hq (%d) must be a multiple of Hkv (%d)",
                  fn, num_qo_heads, num_kv_heads);
@@ -439,7 +443,6 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
               (long long)workspace_bytes);
     return MSGL_ERR_WORKSPACE;
   }
-  DecodeParams p;
   p.q = q;
   p.k_pool = k_pool;
   p.v_pool = v_pool;
@@ -462,13 +465,31 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
   p.part_o = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_o) : nullptr;
   p.batch = batch;
   p.ngrp = decode_groups(num_kv_heads);
-  p.planned = mode == kRunPlanned;
+  p.planned = planned;
   p.num_slots = num_slots;
   p.hq = num_qo_heads;
   p.hkv = num_kv_heads;
   p.page_size = page_size;
   p.max_splits = max_splits;
   p.scale_log2 = scale * kLog2e;
+  return MSGL_OK;
+}
+
+static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, const void* k_new, const void* v_new,
+                             const int32_t* out_loc, const void* k_pool, const void* v_pool, const float* kv_scale,
+                             const int32_t* kv_indptr, const int32_t* kv_indices,
+                             const int32_t* seq_lens,
+                             int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                             int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                             void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  DecodeParams p;
+  bool empty = false;
+  const int st = dec::decode_params(fn, mode == kRunPlanned, q, k_new, v_new, out_loc, k_pool, v_pool, kv_scale,
+                                    kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim,
+                                    page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, p,
+                                    empty);
+  if (st != MSGL_OK || empty) return st;
   const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
   if (kv_scale != nullptr) {  // fp8 e4m3 pools with per-(slot, kv head) scales

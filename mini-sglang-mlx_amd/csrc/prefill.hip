@@ -494,17 +494,22 @@ extern "C" int64_t msgl_prefill_workspace_size(int32_t num_reqs, int32_t num_tok
       .bytes;
 }
 
-namespace {
-int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, const void* v_pool,
-                 const float* kv_scale, const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
-                 const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
-                 int32_t max_seq_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
-                 int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
-                 int64_t workspace_bytes, void* stream) {
-  using namespace msgl;
+// Validates the arguments of a prefill call and fills p (the workspace regions
+// included); empty: the batch has no query, nothing to launch.
+int msgl::pf::prefill_params(const char* fn, int mode, const void* q, const void* k_pool, const void* v_pool,
+                       const float* kv_scale, const int32_t* q_indptr, const int32_t* kv_indptr,
+                       const int32_t* kv_indices, const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens,
+                       int32_t max_extend_len, int32_t max_seq_len, int32_t num_qo_heads, int32_t num_kv_heads,
+                       int32_t head_dim, int32_t page_size, int64_t num_slots, int32_t dtype, float scale,
+                       int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes, PrefillParams& p,
+                       bool& empty) {
   clear_error();
+  empty = false;
   MSGL_CHECK_ARG(num_reqs >= 0 && num_tokens >= 0 && max_extend_len >= 0, "%s: sizes must be >= 0", fn);
-  if (num_reqs == 0 || max_extend_len == 0 || num_tokens == 0) return MSGL_OK;
+  if (num_reqs == 0 || max_extend_len == 0 || num_tokens == 0) {
+    empty = true;
+    return MSGL_OK;
+  }
   MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0, "%s: sizes must be > 0", fn);
   MSGL_CHECK_ARG(num_qo_heads % num_kv_heads == 0, "%s: Hq (%d) must be a multiple of Hkv (%d)", fn, num_qo_heads,
                  num_kv_heads);
@@ -524,7 +529,6 @@ int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, co
     set_error("%s: unknown dtype %d", fn, dtype);
     return MSGL_ERR_UNSUPPORTED;
   }
-  PrefillParams p;
   p.q = q;
   p.k_pool = k_pool;
   p.v_pool = v_pool;
@@ -576,6 +580,24 @@ int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, co
       p.part_o = reinterpret_cast<float*>(ws + w.part_o);
     }
   }
+  return MSGL_OK;
+}
+
+namespace {
+int prefill_impl(const char* fn, int mode, const void* q, const void* k_pool, const void* v_pool,
+                 const float* kv_scale, const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                 const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
+                 int32_t max_seq_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                 int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace,
+                 int64_t workspace_bytes, void* stream) {
+  using namespace msgl;
+  PrefillParams p;
+  bool empty = false;
+  const int st = pf::prefill_params(fn, mode, q, k_pool, v_pool, kv_scale, q_indptr, kv_indptr, kv_indices, seq_lens,
+                                    num_reqs, num_tokens, max_extend_len, max_seq_len, num_qo_heads, num_kv_heads,
+                                    head_dim, page_size, num_slots, dtype, scale, max_splits, out, workspace,
+                                    workspace_bytes, p, empty);
+  if (st != MSGL_OK || empty) return st;
   const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
   if (kv_scale != nullptr) {  // fp8 e4m3 pools with per-(slot, kv head) scales

@@ -802,5 +802,14 @@ __device__ __forceinline__ void prefill_merge_body(const PrefillParams& p, int t
   *reinterpret_cast<uint2*>(dst) = *reinterpret_cast<const uint2*>(r);
 }
 
+// Validates the arguments of a prefill call and fills p (the workspace regions
+// included); empty: the batch has no query, nothing to launch. (prefill.hip)
+int prefill_params(const char* fn, int mode, const void* q, const void* k_pool, const void* v_pool,
+                   const float* kv_scale, const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* kv_indices,
+                   const int32_t* seq_lens, int32_t num_reqs, int32_t num_tokens, int32_t max_extend_len,
+                   int32_t max_seq_len, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
+                   int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
+                   void* workspace, int64_t workspace_bytes, PrefillParams& p, bool& empty);
+
 }  // namespace pf
 }  // namespace msgl

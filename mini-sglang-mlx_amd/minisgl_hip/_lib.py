@@ -132,6 +132,12 @@ SIGNATURES["msgl_paged_decode_store_fp8"] = (
      _c_f, _c_i32, _c_p, _c_p, _c_i64, _c_p],
 )
 SIGNATURES["msgl_paged_decode_store_fp8_planned"] = SIGNATURES["msgl_paged_decode_store_fp8"]
+SIGNATURES["msgl_mixed_attention"] = (
+    ctypes.c_int,
+    [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_p, _c_p, _c_i64,  # decode part
+     _c_p, _c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_i64,  # prefill part
+     _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_f, _c_p],
+)
 
 _lib = None
 

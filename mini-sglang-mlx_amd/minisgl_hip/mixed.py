@@ -15,11 +15,14 @@ Decode requests come first in the packed batch (one token each), prefill
 requests after them; q and out are the packed [T, Hq, D] tensors. Per request
 the results are those of the reference's decode or prefill path.
 
-Steps 3 and 4 touch disjoint output rows and pool rows no other part writes,
-so with ``concurrent`` (the default) the prefill runs on a second stream of
-default priority, forked after step 2 and joined before ``run`` returns: the
-HBM-bound decode and the matrix-core-bound prefill then share the GPU instead
-of running one after the other.
+Steps 3 and 4 touch disjoint output rows and pool rows no other part writes.
+With ``single_launch`` (the default) they are one launch (``msgl_mixed_attention``: one grid
+whose workgroups take decode and prefill work items in proportion, after the
+two work-list plans), plus one merge launch; with ``concurrent`` (and no single
+launch) the prefill runs on a second stream of default priority, forked after
+step 2 and joined before ``run`` returns. Either way the HBM-bound decode and
+the matrix-core-bound prefill share the GPU instead of running one after the
+other, and the results are bit-identical to running them in turn.
 """
 
 from __future__ import annotations
@@ -94,13 +97,19 @@ class MixedStep:
         )
         return self.indices
 
-    def run(self, q, k_new, v_new, k_pool, v_pool, out, scale: float, concurrent: bool = True) -> torch.Tensor:
-        """q, k_new, v_new, out: packed [T, H, D]; the pools are one layer's."""
+    def run(self, q, k_new, v_new, k_pool, v_pool, out, scale: float, concurrent: bool = True,
+            single_launch: bool = True) -> torch.Tensor:
+        """q, k_new, v_new, out: packed [T, H, D]; the pools are one layer's.
+
+        ``single_launch`` (default): decode and prefill in one launch; otherwise
+        two streams (``concurrent``) or one after the other."""
         idx = self.build_indices()
         nd = self.num_decode
         has_prefill = self.num_tokens > nd
         if has_prefill:
             ops.store_kv(k_new[nd:], v_new[nd:], idx["out_loc"][nd:], k_pool, v_pool)
+        if single_launch and has_prefill and nd:
+            return self._run_single(idx, q, k_new, v_new, k_pool, v_pool, out, scale)
 
         def prefill():
             ops.prefill_ragged_attention(
@@ -134,3 +143,23 @@ class MixedStep:
         elif has_prefill and nd:
             prefill()
         return out
+
+    def _run_single(self, idx, q, k_new, v_new, k_pool, v_pool, out, scale: float) -> torch.Tensor:
+        """Both plans, then the decode and the prefill in one launch (``ops.mixed_attention``)."""
+        nd = self.num_decode
+        t, hq, d = q.shape
+        hkv = k_pool.shape[1]
+        ops.paged_decode_plan(idx["kv_indptr"][: nd + 1], self.device_len[:nd], nd, hq, hkv, d, self.decode_splits,
+                              self.decode_ws)
+        ops.prefill_plan(idx["q_indptr"][nd:], idx["kv_indptr"][nd:], self.device_len[nd:], num_tokens=t,
+                         max_extend_len=self.max_chunk, max_seq_len=self.max_seq_len, num_qo_heads=hq,
+                         num_kv_heads=hkv, head_dim=d, dtype=q.dtype, max_splits=self.prefill_splits,
+                         workspace=self.prefill_ws)
+        return ops.mixed_attention(
+            q, k_pool, v_pool, scale, num_decode=nd, dec_kv_indptr=idx["kv_indptr"][: nd + 1],
+            dec_kv_indices=idx["kv_indices"], dec_seq_lens=self.device_len[:nd], dec_max_splits=self.decode_splits,
+            dec_workspace=self.decode_ws, new_kv=(k_new[:nd], v_new[:nd], idx["out_loc"][:nd]),
+            q_indptr=idx["q_indptr"][nd:], pf_kv_indptr=idx["kv_indptr"][nd:], pf_kv_indices=idx["kv_indices"],
+            pf_seq_lens=self.device_len[nd:], max_extend_len=self.max_chunk, max_seq_len=self.max_seq_len,
+            pf_max_splits=self.prefill_splits, pf_workspace=self.prefill_ws, page_size=self.page_size, out=out,
+        )

@@ -397,6 +397,82 @@ def prefill_plan(
     _lib.check(status, "msgl_prefill_plan")
 
 
+def mixed_attention(
+    q: torch.Tensor,
+    k_pool: torch.Tensor,
+    v_pool: torch.Tensor,
+    scale: float,
+    *,
+    num_decode: int,
+    dec_kv_indptr: torch.Tensor,
+    dec_kv_indices: torch.Tensor,
+    dec_seq_lens: Optional[torch.Tensor],
+    dec_max_splits: int,
+    dec_workspace: torch.Tensor,
+    new_kv: Optional[tuple],
+    q_indptr: torch.Tensor,
+    pf_kv_indptr: torch.Tensor,
+    pf_kv_indices: torch.Tensor,
+    pf_seq_lens: Optional[torch.Tensor],
+    max_extend_len: int,
+    max_seq_len: int,
+    pf_max_splits: int,
+    pf_workspace: torch.Tensor,
+    page_size: int = 1,
+    out: Optional[torch.Tensor] = None,
+) -> torch.Tensor:
+    """A mixed batch's decode and prefill attention in one launch (+ one merge launch).
+
+    q/out: the packed [T, Hq, D] batch, decode requests first (rows [0, num_decode),
+    one token each), the prefill chunks after them at the packed offsets of
+    ``q_indptr``. ``new_kv = (k_new, v_new, out_loc)`` ([num_decode, Hkv, D] and
+    [num_decode]) stores the decode requests' new rows in the same launch. The
+    work lists must already be in the workspaces (``paged_decode_plan`` and
+    ``prefill_plan`` over the same indices). Per request the result is that of
+    ``paged_decode_attention`` / ``prefill_ragged_attention``."""
+    if q.dim() != 3 or k_pool.dim() != 3 or k_pool.shape != v_pool.shape:
+        raise ValueError("q must be [T, Hq, D] and pools [N, Hkv, D]")
+    t, hq, d = q.shape
+    n_slots, hkv, dk = k_pool.shape
+    if dk != d or hq % hkv != 0 or len({q.dtype, k_pool.dtype, v_pool.dtype}) != 1:
+        raise ValueError("q and pools must share head_dim and dtype, Hq a multiple of Hkv")
+    if not 0 <= num_decode <= t:
+        raise ValueError("num_decode must be in [0, T]")
+    dev = q.device
+    for name, x in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
+        _check_device(name, x, dev)
+    for name, x in (("dec_kv_indptr", dec_kv_indptr), ("dec_kv_indices", dec_kv_indices),
+                    ("dec_seq_lens", dec_seq_lens), ("q_indptr", q_indptr), ("pf_kv_indptr", pf_kv_indptr),
+                    ("pf_kv_indices", pf_kv_indices), ("pf_seq_lens", pf_seq_lens)):
+        _check_index(name, x, dev)
+    if out is None:
+        out = torch.empty_like(q)
+    elif out.shape != q.shape or out.dtype != q.dtype:
+        raise ValueError("out must match q's shape and dtype")
+    k_new = v_new = out_loc = None
+    if new_kv is not None:
+        k_new, v_new, out_loc = new_kv
+        if k_new.shape != (num_decode, hkv, d) or v_new.shape != k_new.shape or out_loc.shape != (num_decode,):
+            raise ValueError("k_new/v_new must be [num_decode, Hkv, D] and out_loc [num_decode]")
+        if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+            raise ValueError("k_new/v_new must share q's dtype")
+        _check_device("k_new", k_new, dev)
+        _check_device("v_new", v_new, dev)
+        _check_index("out_loc", out_loc, dev)
+    status = _lib.load().msgl_mixed_attention(
+        _lib.ptr(q), _lib.ptr(k_new), _lib.ptr(v_new), _lib.ptr(out_loc), _lib.ptr(dec_kv_indptr),
+        _lib.ptr(dec_kv_indices), _lib.ptr(dec_seq_lens), int(num_decode), int(dec_max_splits), _lib.ptr(out),
+        _lib.ptr(dec_workspace), dec_workspace.numel() * dec_workspace.element_size(),
+        _lib.ptr(q), _lib.ptr(q_indptr), _lib.ptr(pf_kv_indptr), _lib.ptr(pf_kv_indices), _lib.ptr(pf_seq_lens),
+        q_indptr.shape[0] - 1, t, int(max_extend_len), int(max_seq_len), int(pf_max_splits), _lib.ptr(out),
+        _lib.ptr(pf_workspace), pf_workspace.numel() * pf_workspace.element_size(),
+        _lib.ptr(k_pool), _lib.ptr(v_pool), hq, hkv, d, int(page_size), n_slots, _lib.dtype_code(q.dtype),
+        float(scale), _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_mixed_attention")
+    return out
+
+
 def build_step_indices(
     req_to_token: torch.Tensor,
     table_idx: torch.Tensor,

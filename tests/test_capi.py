@@ -170,6 +170,15 @@ def test_host_side_argument_errors():
     assert dsf(loc=nul) == _lib.MSGL_ERR_INVALID and "out_loc" in _lib.last_error()
     assert dsf(kn=24) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
     assert dsf(dtype=0) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()
+    # mixed step: (decode part ..., prefill part ..., pools, Hq, Hkv, D, page, slots, dtype, scale, stream)
+    mx = lambda nd=4, npf=2, kn=16, loc=16, dtype=1: lib.msgl_mixed_attention(  # noqa: E731
+        16, kn, kn, loc, 16, 16, nul, nd, 1, 16, 256, 1 << 30,
+        16, 16, 16, 16, nul, npf, 64, 32, 0, 1, 16, 256, 1 << 30,
+        16, 16, 16, 8, 128, 1, 100, dtype, 0.1, nul)
+    assert mx(nd=-1) == _lib.MSGL_ERR_INVALID
+    assert mx(dtype=0) == _lib.MSGL_ERR_UNSUPPORTED and "bf16 or fp16" in _lib.last_error()
+    assert mx(loc=nul) == _lib.MSGL_ERR_INVALID and "out_loc" in _lib.last_error()
+    assert mx(kn=24) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
     # fp8 prefill: (q, kp, vp, kv_scale, q_indptr, kv_indptr, kv_indices, seq_lens, R, T, maxE, maxL, Hq, Hkv, D,
     #               page, slots, dtype, scale, splits, out, ws, ws_bytes, stream)
     pf8 = lambda dtype=1, sc=16, d=128: lib.msgl_prefill_ragged_fp8(  # noqa: E731

@@ -67,9 +67,14 @@ def test_mixed_step_small(cuda_device):
     kn = randn((t, HKV, D), 63, dt).to(cuda_device)
     vn = randn((t, HKV, D), 64, dt).to(cuda_device)
     out = torch.empty_like(q)
+    kp1, vp1 = kp.clone(), vp.clone()
     step = _step(case, cuda_device, int(case.device_len.max()))
-    step.run(q, kn, vn, kp, vp, out, SCALE)
+    step.run(q, kn, vn, kp, vp, out, SCALE, single_launch=False)  # two streams
+    out1 = torch.empty_like(q)
+    step.run(q, kn, vn, kp1, vp1, out1, SCALE, single_launch=True)
     torch.cuda.synchronize()
+    assert torch.equal(out, out1), "the single-launch step differs from the two-stream step"
+    assert torch.equal(kp, kp1) and torch.equal(vp, vp1), "the single-launch step stored different rows"
     # the step's rows are in the pool at the slots of positions [cached, device)
     positions, out_loc = oracle.prepare_batch_indices(case.req_to_token, case.table_idx, case.cached_len,
                                                       case.device_len)
@@ -95,14 +100,18 @@ def test_mixed_step_full_size(cuda_device):
     vn = torch.randn((t, HKV, D), generator=g, device=cuda_device, dtype=dt)
     out = torch.empty_like(q)
     step = _step(case, cuda_device, int(case.device_len.max()))
-    step.run(q, kn, vn, kp, vp, out, SCALE)
+    step.run(q, kn, vn, kp, vp, out, SCALE, single_launch=False)  # two streams
     out2 = torch.empty_like(q)
-    step.run(q, kn, vn, kp, vp, out2, SCALE)
+    step.run(q, kn, vn, kp, vp, out2, SCALE, single_launch=False)
     out3 = torch.empty_like(q)
-    step.run(q, kn, vn, kp, vp, out3, SCALE, concurrent=False)  # decode, then prefill, on one stream
+    step.run(q, kn, vn, kp, vp, out3, SCALE, concurrent=False, single_launch=False)  # decode, then prefill
+    out4 = torch.empty_like(q)
+    print("case mixed full single launch", flush=True)
+    step.run(q, kn, vn, kp, vp, out4, SCALE, single_launch=True)  # one grid for both
     torch.cuda.synchronize()
     assert torch.equal(out, out2), "mixed step is not deterministic"
     assert torch.equal(out, out3), "the two-stream step differs from the one-stream order"
+    assert torch.equal(out, out4), "the single-launch step differs from the one-stream order"
     longest = int(np.argmax(case.device_len[: case.num_decode]))
     for i in sorted({0, 5, longest, case.num_decode - 1}):
         _check_request(case, i, q, kp, vp, out)
@@ -110,3 +119,35 @@ def test_mixed_step_full_size(cuda_device):
         _check_request(case, i, q, kp, vp, out, rows=64)
     del kp, vp
     torch.cuda.empty_cache()
+
+
+@pytest.mark.parametrize("hq,hkv,d,page", [(16, 8, 128, 1), (32, 8, 128, 16), (8, 2, 64, 1), (16, 16, 128, 16)])
+def test_mixed_single_launch_shapes(cuda_device, hq, hkv, d, page):
+    """msgl_mixed_attention over head groups 1..4, head_dim 64/128, pages 1/16, fp16
+    and bf16: bit-identical to the decode and prefill calls run in turn, and the
+    oracle for every request."""
+    case = workloads.mixed_case(6, 20, 900, [0, 100, 1500], 96, num_slots=32768, page_size=page, seed=hq + d)
+    for dt in (torch.bfloat16, torch.float16):
+        print(f"case mixed single {hq}/{hkv}/{d} page={page} {dt}", flush=True)
+        kp = randn((case.num_slots, hkv, d), 80, dt).to(cuda_device)
+        vp = randn((case.num_slots, hkv, d), 81, dt).to(cuda_device)
+        t = case.num_tokens
+        q = randn((t, hq, d), 82, dt).to(cuda_device)
+        kn = randn((t, hkv, d), 83, dt).to(cuda_device)
+        vn = randn((t, hkv, d), 84, dt).to(cuda_device)
+        step = MixedStep(
+            i32(case.req_to_token, cuda_device), i32(case.table_idx, cuda_device), i32(case.cached_len, cuda_device),
+            i32(case.device_len, cuda_device), num_decode=case.num_decode, num_tokens=t, num_pages=case.num_pages,
+            max_chunk=case.max_chunk, max_seq_len=int(case.device_len.max()), num_qo_heads=hq, num_kv_heads=hkv,
+            head_dim=d, page_size=page,
+        )
+        kp1, vp1 = kp.clone(), vp.clone()
+        a = torch.empty_like(q)
+        step.run(q, kn, vn, kp, vp, a, d**-0.5, concurrent=False, single_launch=False)
+        b = torch.empty_like(q)
+        step.run(q, kn, vn, kp1, vp1, b, d**-0.5, single_launch=True)
+        torch.cuda.synchronize()
+        assert torch.equal(a, b) and torch.equal(kp, kp1) and torch.equal(vp, vp1)
+        if dt == torch.bfloat16 and hq == HQ and hkv == HKV and d == D:
+            for i in range(case.num_reqs):
+                _check_request(case, i, q, kp, vp, b)
