@@ -9,13 +9,17 @@
 // prefill body on one work item of the lists msgl_paged_decode_plan and
 // msgl_prefill_plan built.
 //
-// Workgroup i takes prefill item floor(i nP / (nP + nD)) when that count steps
-// up at i, otherwise decode item i - floor(i nP / (nP + nD)) (nP, nD: the list
-// lengths the plans left in the workspaces): the two longest-first lists
-// interleave in proportion, so CUs hold HBM-bound decode and matrix-core-bound
-// prefill workgroups side by side from the first wave of dispatch on. Both
-// bodies run as 4-wavefront workgroups; the launch takes the larger LDS of the
-// two (the prefill ring) and the prefill's register budget.
+// The grid is cut into groups of 8 workgroups (workgroup i runs on XCD i % 8).
+// Group c is a prefill group when floor(c P / (P + Q)) steps up at c (P, Q:
+// the prefill and decode lists' lengths in groups of 8, from the list lengths
+// the plans left in the workspaces), otherwise a decode group; workgroup j of
+// the k-th group of a kind takes item 8k + j of that list. The two
+// longest-first lists interleave in proportion, so CUs hold HBM-bound decode
+// and matrix-core-bound prefill workgroups side by side from the first wave of
+// dispatch on, and each item runs on the XCD it runs on in its own kernel
+// (item % 8: a prefill head's query blocks share one L2). Both bodies run as
+// 4-wavefront workgroups; the launch takes the larger LDS of the two (the
+// prefill ring) and the prefill's register budget.
 #include "decode_device.h"
 #include "prefill_device.h"
 
@@ -27,15 +31,18 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf::G16<D>:
     pf::PrefillParams pp, dec::DecodeParams dp) {
   const int np = *pp.plan_count;
   const int nd = dp.meta[0];
-  const int i = blockIdx.x;
-  if (i >= np + nd) return;
-  const int64_t tot = (int64_t)np + nd;
-  const int a = (int)((int64_t)i * np / tot);
-  const int a1 = (int)((int64_t)(i + 1) * np / tot);
+  const int gp = (np + 7) >> 3, gd = (nd + 7) >> 3;
+  const int c = blockIdx.x >> 3, j = blockIdx.x & 7;
+  if (c >= gp + gd) return;
+  const int64_t tot = (int64_t)gp + gd;
+  const int a = (int)((int64_t)c * gp / tot);
+  const int a1 = (int)((int64_t)(c + 1) * gp / tot);
   if (a1 > a) {
-    pf::prefill16_body<T, T, D, G>(pp, a);
+    const int item = 8 * a + j;
+    if (item < np) pf::prefill16_body<T, T, D, G>(pp, item);
   } else {
-    dec::paged_decode_body<T, T, D, G>(dp, i - a);
+    const int item = 8 * (c - a) + j;
+    if (item < nd) dec::paged_decode_body<T, T, D, G>(dp, item);
   }
 }
 
@@ -76,8 +83,9 @@ int launch_mixed(pf::PrefillParams pp, const dec::DecodeParams& dp, int batch, i
     }
     attr_set = true;
   }
-  hipLaunchKernelGGL((mixed_attention_kernel<T, D, G>), dim3((unsigned)(items_pf + items_dec)), dim3(256), lds,
-                     stream, pp, dp);
+  const int64_t groups = (items_pf + 7) / 8 + (items_dec + 7) / 8;
+  hipLaunchKernelGGL((mixed_attention_kernel<T, D, G>), dim3((unsigned)(8 * groups)), dim3(256), lds, stream, pp,
+                     dp);
   MSGL_CHECK_LAUNCH("msgl_mixed_attention");
   constexpr int HPB = 256 / (D / 4);  // heads per prefill-merge workgroup
   const int npm = pp.splits > 1 ? pp.num_tokens * ((pp.hq + HPB - 1) / HPB) : 0;
