@@ -97,6 +97,26 @@ __device__ __forceinline__ int slot_of(const int32_t* __restrict__ kv_indices, i
   return (s >= 0 && s < num_slots) ? (int)s : 0;
 }
 
+// Balanced split: the length of one key range of the batch's concatenated
+// token stream (requests in order, ttot keys in all) when nranges ranges cover
+// it: ceil(ttot / nranges), but at least ceil(max_len / (max_splits - 1)) so no
+// request overlaps more than max_splits ranges (the partials the workspace
+// holds per request) and at least kMinChunk keys. Used identically by the
+// decode and merge kernels.
+__device__ __forceinline__ int64_t balanced_range(int64_t ttot, int max_len, int nranges, int max_splits) {
+  int64_t r = (ttot + nranges - 1) / nranges;
+  r = max(r, ((int64_t)max_len + max_splits - 2) / (max_splits - 1));
+  return max(r, (int64_t)kMinChunk);
+}
+
+// A balanced launch is used when the ranges average at least this many keys:
+// shorter ranges measured slower on MI355X than per-request chunks (each chunk
+// pays its slot staging, fold and partial store, and the merge reads more
+// partials), longer ones faster (ragged long contexts leave no tail).
+#ifndef MSGL_DECODE_BALANCED_MIN_RANGE
+#define MSGL_DECODE_BALANCED_MIN_RANGE 2048
+#endif
+
 struct DecodeParams {
   const void* q;
   const void* k_pool;
@@ -116,13 +136,24 @@ struct DecodeParams {
   void* k_pool_w;
   void* v_pool_w;
   // work list (plan kernel output, in the workspace)
-  int* meta;        // [0] items in the plan, [1] batch-wide chunk length
+  int* meta;        // [0] items in the plan, [1] batch-wide chunk length, [3] max_b L_b
   int4* plan;       // (request, split, kv-head group, 0), longest first
+  int64_t* tok_off; // balanced split: [B+1] tokens of the requests before b (tok_off[B] = all)
+  int nranges;      // balanced split: key ranges of the launch (grid / ngrp)
   int64_t num_slots;
   int hq, hkv, page_size, max_splits, batch, ngrp;
-  bool planned;  // the workspace already holds this call's plan
+  bool planned;   // the workspace already holds this call's plan
+  bool balanced;  // equal key ranges of the batch's token stream allowed (else per-request chunks)
   float scale_log2;
 };
+
+// Whether this launch splits by equal key ranges: allowed, and the batch's
+// keys (tok_off[B], from the plan) average at least
+// MSGL_DECODE_BALANCED_MIN_RANGE per range. Used identically by the decode and
+// merge kernels; otherwise both follow the per-request work list.
+__device__ __forceinline__ bool balanced_launch(const DecodeParams& p) {
+  return p.balanced && p.tok_off[p.batch] >= (int64_t)MSGL_DECODE_BALANCED_MIN_RANGE * p.nranges;
+}
 
 // LDS per wavefront: P tile [16 tokens][16 rows] + alpha[16] + (m, l)[16 rows].
 constexpr int kLdsPerWave = 16 * 16 + 16 + 32;
@@ -158,8 +189,10 @@ constexpr int k_lds_stride() { return D * (int)sizeof(KV) + 16; }
 #endif
 
 // T: the query/output type; KV: the pool's storage type (T itself, or fp8e4m3
-// for a quantised pool with per-(slot, kv head) scales).
-template <typename T, typename KV, int D, int G>
+// for a quantised pool with per-(slot, kv head) scales). RANGES: the key-range
+// form is built in (its chunk loop costs registers; without it every
+// workgroup runs one work-list item and p.balanced must be false).
+template <typename T, typename KV, int D, int G, bool RANGES>
 __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg) {
   constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
   constexpr int VEC = QK<T>::VEC;   // query elements per 16-byte chunk (MFMA operand)
@@ -192,37 +225,22 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
   float* ML_lds = lds + 256 + 16;  // [16][2]
   uint8_t* K_lds = reinterpret_cast<uint8_t*>(lds + kLdsPerWave);  // [16][KRS bytes]
 
-  // work item from the plan (workgroups past its end have nothing to do); a
-  // kv-head group is this workgroup's waves
-  if (wg >= p.meta[0]) return;
-  const int4 item = p.plan[wg];
-  const int b = item.x;
-  const int split = item.y;
-  const int kgrp = item.z;
-  const int start = p.kv_indptr[b];
-  const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - start;
-  int n, chunk;
-  split_geometry(L, p.max_splits, p.meta[1], n, chunk);
-  if (split >= n) {
-    if (split == 0) {  // L == 0: defined zero output for this group's heads
-      const int h0 = kgrp * nwaves * G;
-      const int h1 = min(p.hq, h0 + nwaves * G);
-      T* o = reinterpret_cast<T*>(p.out) + (int64_t)b * p.hq * D;
-      for (int i = h0 * D + threadIdx.x; i < h1 * D; i += blockDim.x) o[i] = from_f32<T>(0.f);
-    }
-    return;
-  }
-  const int t0 = split * chunk;
-  const int t1 = split == n - 1 ? L : t0 + chunk;
-
-  const int r = lane & 15;    // MFMA column (token in tile) / A row
-  const int g4 = lane >> 4;   // MFMA row group
-  const int vc = lane % LPR;  // V: 16-byte chunk within the row
-  const int vr = lane / LPR;  // V: token sub-row
-
   const int64_t row_stride = (int64_t)p.hkv * D * EKV;  // bytes per slot
 
+  // One chunk: keys [t0, t1) of request b (L keys, kv_indices from start),
+  // partial `split` of its n; the kv-head group kgrp is this workgroup's waves.
+  auto run_chunk = [&](const int b, const int start, const int L, const int t0, const int t1, const int split,
+                       const int n, const int kgrp) {
   {
+    // lane-derived indices are recomputed per chunk from an opaque copy of
+    // the lane id: hoisted out of the chunk loop they would hold registers
+    // through the whole tile loop
+    int lid = lane;
+    if constexpr (RANGES) asm volatile("" : "+v"(lid));
+    const int r = lid & 15;    // MFMA column (token in tile) / A row
+    const int g4 = lid >> 4;   // MFMA row group
+    const int vc = lid % LPR;  // V: 16-byte chunk within the row
+    const int vr = lid / LPR;  // V: token sub-row
     const int kvh = kgrp * nwaves + wave;
     const bool active = kvh < p.hkv;
     const int kvh_c = active ? kvh : 0;
@@ -463,6 +481,79 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
       p.part_ml[(base + lane) * 2 + 1] = ML_lds[lane * 2 + 1];
     }
   }
+  };
+
+  // This workgroup's chunks, run one after another through one call site.
+  // Balanced: key range k of the batch's token stream (requests concatenated
+  // in order), all ranges of one length, for kv-head group kgrp -- every
+  // workgroup gets the same number of keys, so the launch ends when the
+  // average one does. A range can span request boundaries: each request's part
+  // is a chunk of its own, partial (k - the request's first range) of the
+  // ranges it overlaps. Otherwise: one work item of the plan (workgroups past
+  // its end have nothing to do).
+  const bool bal = RANGES && balanced_launch(p);
+  int b, kgrp, start = 0, L = 0, t0 = 0, t1 = 0, split = 0, n = 1;
+  int64_t k = 0, rl = 1, g0 = 0, g1 = 0;
+  if (bal) {
+    kgrp = wg % p.ngrp;
+    k = wg / p.ngrp;
+    const int64_t ttot = p.tok_off[p.batch];
+    rl = balanced_range(ttot, p.meta[3], p.nranges, p.max_splits);
+    g0 = k * rl;
+    g1 = min(ttot, g0 + rl);
+    if (g0 >= g1) return;
+    // the last request starting at or before key g0 (it holds key g0): a
+    // 64-way search, every lane probes one offset per round, so a batch of up
+    // to 4096 requests takes two dependent loads
+    int lo = 0, hi = p.batch - 1;
+    while (lo < hi) {
+      const int step = (hi - lo + 64) >> 6;
+      const int idx = lo + lane * step;
+      const uint64_t ok = __ballot(idx <= hi && p.tok_off[idx] <= g0);  // a prefix of the lanes, lane 0 included
+      lo += (63 - __clzll((long long)ok)) * step;
+      hi = min(hi, lo + step - 1);
+    }
+    b = lo;
+  } else {
+    if (wg >= p.meta[0]) return;
+    const int4 item = p.plan[wg];
+    b = item.x;
+    split = item.y;
+    kgrp = item.z;
+    start = p.kv_indptr[b];
+    L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - start;
+    int chunk;
+    split_geometry(L, p.max_splits, p.meta[1], n, chunk);
+    if (split >= n) {
+      if (split == 0) {  // L == 0: defined zero output for this group's heads
+        const int h0 = kgrp * nwaves * G;
+        const int h1 = min(p.hq, h0 + nwaves * G);
+        T* o = reinterpret_cast<T*>(p.out) + (int64_t)b * p.hq * D;
+        for (int i = h0 * D + threadIdx.x; i < h1 * D; i += blockDim.x) o[i] = from_f32<T>(0.f);
+      }
+      return;
+    }
+    t0 = split * chunk;
+    t1 = split == n - 1 ? L : t0 + chunk;
+  }
+  for (;; ++b) {
+    if (bal) {
+      if (g0 >= g1 || b >= p.batch) return;
+      const int64_t ob = p.tok_off[b], ob1 = p.tok_off[b + 1];
+      if (ob1 <= g0) continue;  // no key of b in the range (L = 0)
+      const int64_t s1 = min(g1, ob1);
+      start = p.kv_indptr[b];
+      L = (int)(ob1 - ob);
+      t0 = (int)(g0 - ob);
+      t1 = (int)(s1 - ob);
+      split = (int)(k - ob / rl);
+      n = (int)((ob1 - 1) / rl - ob / rl + 1);
+      g0 = s1;
+    }
+    run_chunk(b, start, L, t0, t1, split, n, kgrp);
+    if constexpr (!RANGES) return;
+    if (!bal) return;
+  }
 }
 
 // Merge split-K partials, one wavefront per (request, kv head):
@@ -476,9 +567,20 @@ __device__ __forceinline__ void paged_decode_merge_body(const DecodeParams& p, i
   const int lane = threadIdx.x & 63;
   if (unit >= batch * p.hkv) return;
   const int b = unit / p.hkv, kvh = unit % p.hkv;
-  const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];
   int n, chunk;
-  split_geometry(L, p.max_splits, p.meta[1], n, chunk);
+  if (balanced_launch(p)) {  // the ranges request b overlaps; no key: the defined zero output
+    const int64_t ob = p.tok_off[b], ob1 = p.tok_off[b + 1];
+    if (ob1 == ob) {
+      T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D;
+      for (int i = lane; i < G * D; i += 64) o[i] = from_f32<T>(0.f);
+      return;
+    }
+    const int64_t rl = balanced_range(p.tok_off[p.batch], p.meta[3], p.nranges, p.max_splits);
+    n = (int)((ob1 - 1) / rl - ob / rl + 1);
+  } else {
+    const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];
+    split_geometry(L, p.max_splits, p.meta[1], n, chunk);
+  }
   if (n <= 1) return;
   const int64_t bbase = (int64_t)b * p.max_splits * p.hq + kvh * G;
   constexpr int C4 = D / 4;
@@ -549,6 +651,10 @@ int decode_params(const char* fn, bool planned, const void* q, const void* k_new
                   int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
                   int32_t dtype, float scale, int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
                   DecodeParams& p, bool& empty);
+
+// Workgroups of the decode launch (p.nranges key ranges x p.ngrp kv-head
+// groups when balanced, else one per plan item). (paged_decode.hip)
+int64_t decode_items(const DecodeParams& p);
 
 }  // namespace dec
 }  // namespace msgl

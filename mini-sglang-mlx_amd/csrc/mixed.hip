@@ -7,7 +7,7 @@
 // new token's store of kvcache/pool.py:47-50 fused in) or of the prefill path
 // (attention/base.py:85-105): each workgroup runs the unchanged decode or
 // prefill body on one work item of the lists msgl_paged_decode_plan and
-// msgl_prefill_plan built.
+// msgl_prefill_plan built (the decode part always runs per-request chunks).
 //
 // The grid is cut into groups of 8 workgroups (workgroup i runs on XCD i % 8).
 // Group c is a prefill group when floor(c P / (P + Q)) steps up at c (P, Q:
@@ -42,7 +42,7 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf::G16<D>:
     if (item < np) pf::prefill16_body<T, T, D, G>(pp, item);
   } else {
     const int item = 8 * (c - a) + j;
-    if (item < nd) dec::paged_decode_body<T, T, D, G>(dp, item);
+    if (item < nd) dec::paged_decode_body<T, T, D, G, false>(dp, item);
   }
 }
 
@@ -72,7 +72,7 @@ int launch_mixed(pf::PrefillParams pp, const dec::DecodeParams& dp, int batch, i
     return MSGL_ERR_WORKSPACE;
   }
   pp.items = (int)items_pf;
-  const int64_t items_dec = (int64_t)batch * dp.max_splits * dp.ngrp;
+  const int64_t items_dec = dec::decode_items(dp);
   const size_t lds = std::max<size_t>(Geo::LDS_BYTES, dec::decode_lds_bytes<T, D>(4));
   static bool attr_set = false;  // per process; the attribute is per function
   if (lds > 65536 && !attr_set) {
@@ -203,6 +203,10 @@ extern "C" int msgl_mixed_attention(const void* q_dec, const void* k_new, const 
                           head_dim, page_size, num_slots, dtype, scale, dec_max_splits, out_dec, dec_workspace,
                           dec_workspace_bytes, dp, empty);
   if (st != MSGL_OK) return st;
+  // The decode part follows the per-request work list: key ranges sized for
+  // the decode kernel's own residency would not all fit beside the prefill
+  // items (measured slower), and the list keeps the longest items first.
+  dp.balanced = false;
   const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
   return dtype == MSGL_BF16 ? mixed_dim<bf16_t>(pp, dp, num_decode, max_extend_len, head_dim, group, s)

@@ -10,12 +10,21 @@
 //    finishes; the kv heads of one (b, s) are neighbouring workgroups, so the
 //    rows of a slot (Hkv * D contiguous elements) are read close in time. A
 //    workgroup gathers its token slots once into LDS.
-//  * Split-K: every request is cut into chunks of one batch-wide length,
-//    ceil(max_b L_b / max_splits) rounded to 16 tokens (>= kMinChunk), so a
-//    workgroup never gathers more than one chunk; a one-workgroup plan kernel
-//    lists the (request, chunk, kv-head group) items longest first, so the
-//    grid has no empty workgroups and the long items start first. A
-//    single-chunk request writes its final row. Otherwise every chunk writes
+//  * Split-K, two forms. Per-request chunks: every request is cut into chunks
+//    of one batch-wide length, ceil(max_b L_b / s) rounded to 16 tokens
+//    (>= kMinChunk), and a one-workgroup plan kernel lists the (request,
+//    chunk, kv-head group) items longest first, so the grid has no empty
+//    workgroups and the long items start first. Equal key ranges (long
+//    contexts: at least MSGL_DECODE_BALANCED_MIN_RANGE keys per range): the
+//    batch's keys, requests concatenated in order, are cut into as many
+//    ranges of one length as the device holds workgroups at once (per kv-head
+//    group), so every workgroup gathers the same number of keys and no tail
+//    of long chunks is left running on a few CUs; a range that crosses request
+//    boundaries runs one chunk per request it touches, and the range length
+//    is at least ceil(max_b L_b / (max_splits - 1)), so a request overlaps at
+//    most max_splits ranges. The plan writes the requests' key offsets (a
+//    prefix sum of L) as well as the list; the decode launch picks the form.
+//    A request in one chunk writes its final row; otherwise each chunk writes
 //    fp32 partials (acc, m, l) and a merge kernel with one wavefront per
 //    (request, kv head) combines them. Merging inside the decode launch was
 //    measured slower on MI355X: a device-scope fence per chunk writes back and
@@ -44,13 +53,35 @@
 //    on MI355X than default-policy loads.
 #include "decode_device.h"
 
+// 0: no key-range form; split per request in chunks of one batch-wide length.
+#ifndef MSGL_DECODE_BALANCED
+#define MSGL_DECODE_BALANCED 1
+#endif
+
 namespace msgl {
 using namespace dec;
 
+// Occupancy floor: 16-bit queries with D <= 128 and up to 2 query heads per kv
+// head fit 3 wavefronts per SIMD (168 VGPRs) without spilling, which keeps
+// more K/V loads in flight per CU; the rest keep MSGL_DECODE_MIN_WAVES.
+template <typename T, int D, int G>
+constexpr int decode_min_waves() {
+  return (sizeof(T) == 2 && D <= 128 && G <= 2 && MSGL_DECODE_MIN_WAVES < 3) ? 3 : MSGL_DECODE_MIN_WAVES;
+}
+
+// Instantiations with the key-range form built in: the shapes where its chunk
+// loop (10-25 more VGPRs) leaves the occupancy as it is -- 16-bit queries,
+// head_dim 128, up to 8 query heads per kv head (2 or 4 over fp8 pools).
 template <typename T, typename KV, int D, int G>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(MSGL_DECODE_MIN_WAVES)))
+constexpr bool decode_ranges() {
+  constexpr bool q8 = std::is_same<KV, fp8e4m3>::value;
+  return MSGL_DECODE_BALANCED && sizeof(T) == 2 && D == 128 && (q8 ? (G == 2 || G == 4) : G <= 8);
+}
+
+template <typename T, typename KV, int D, int G>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_min_waves<T, D, G>())))
 void paged_decode_kernel(DecodeParams p) {
-  paged_decode_body<T, KV, D, G>(p, blockIdx.x);
+  paged_decode_body<T, KV, D, G, decode_ranges<T, KV, D, G>()>(p, blockIdx.x);
 }
 
 template <typename T, int D, int G>
@@ -58,8 +89,12 @@ __global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p,
   paged_decode_merge_body<T, D, G>(p, batch, blockIdx.x);
 }
 
-// Work list for paged_decode_kernel, one workgroup: the batch-wide chunk length
-// ceil(max_b L_b / max_splits) (a multiple of 16, >= kMinChunk), then every
+// Plan for paged_decode_kernel, one workgroup. When key ranges are allowed
+// (max_splits > 1): tok_off[b] = sum of L over the requests before b
+// (tok_off[B] = all keys) and meta[3] = max_b L_b. Always the work list (the
+// decode launch picks the form from tok_off[B]): the batch-wide chunk length
+// ceil(max_b L_b / s) (s = max_splits, or chunk_splits when key ranges are
+// allowed; a multiple of 16, >= kMinChunk), then every
 // (request, chunk) counting-sorted by its 16-token tile count, longest first,
 // each expanded to the kv-head groups as consecutive items. Every workgroup
 // then gathers at most one chunk, the long ones are dispatched first and no
@@ -78,12 +113,63 @@ __device__ __forceinline__ int decode_item_tiles(int L, int max_splits, int spli
   return (len + 15) / 16;
 }
 
+// Chunks per request of the work list when the launch may also split by key
+// ranges (max_splits then bounds the ranges, not the chunks): ~4096
+// wavefronts in all, a bit over one round of MI355X at 3 per SIMD, enough
+// units for ragged lengths to balance and few enough that the partials and
+// the merge stay small; no chunk shorter than kMinChunk and none longer than
+// 2048 keys (long contexts need more items than resident slots).
+__device__ __forceinline__ int chunk_splits(int batch, int hkv, int max_len, int max_splits) {
+  const int64_t units = (int64_t)batch * hkv;
+  int64_t s = (4096 + units - 1) / units;
+  s = min(s, (int64_t)(max_len + kMinChunk - 1) / kMinChunk);
+  s = max(s, (int64_t)(max_len + 2047) / 2048);
+  return (int)max((int64_t)1, min(s, (int64_t)max_splits));
+}
+
 __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeParams p) {
   __shared__ int lens[kPlanLds];
   __shared__ int hist[256];
   __shared__ int wmax[kPlanThreads / 64];
+  __shared__ int64_t wsum[kPlanThreads / 64];
   __shared__ int chunk_s;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  if (p.max_splits > 1) {
+    // thread i sums the lengths of a contiguous block of requests; a block
+    // scan turns the sums into exclusive offsets
+    const int per = (p.batch + kPlanThreads - 1) / kPlanThreads;
+    const int b0 = min(p.batch, (int)threadIdx.x * per), b1 = min(p.batch, b0 + per);
+    auto len = [&](int b) { return p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b]; };
+    int64_t sum = 0;
+    int mx = 0;
+    for (int b = b0; b < b1; ++b) {
+      const int L = max(0, len(b));
+      sum += L;
+      mx = max(mx, L);
+    }
+    int64_t incl = sum;
+    for (int d = 1; d < 64; d <<= 1) {
+      const int64_t y = __shfl_up(incl, d);
+      if (lane >= d) incl += y;
+    }
+    for (int d = 32; d >= 1; d >>= 1) mx = max(mx, __shfl_xor(mx, d));
+    if (lane == 63) wsum[wave] = incl;
+    if (lane == 0) wmax[wave] = mx;
+    __syncthreads();
+    int64_t off = incl - sum;
+    for (int w = 0; w < wave; ++w) off += wsum[w];
+    for (int b = b0; b < b1; ++b) {
+      p.tok_off[b] = off;
+      off += max(0, len(b));
+    }
+    if (threadIdx.x == kPlanThreads - 1) p.tok_off[p.batch] = off;  // b1 == batch for the last thread
+    if (threadIdx.x == 0) {
+      int m = 0;
+      for (int w = 0; w < kPlanThreads / 64; ++w) m = max(m, wmax[w]);
+      p.meta[3] = m;
+    }
+    __syncthreads();  // wmax is reused below
+  }
   const bool staged = p.batch <= kPlanLds;
   auto len_of = [&](int b) {
     return staged ? lens[b] : (p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b]);
@@ -101,7 +187,9 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeP
   if (threadIdx.x == 0) {
     int mx = 0;
     for (int w = 0; w < kPlanThreads / 64; ++w) mx = max(mx, wmax[w]);
-    int c = (mx + p.max_splits - 1) / p.max_splits;
+    const int s = MSGL_DECODE_BALANCED && p.max_splits > 1 ? chunk_splits(p.batch, p.hkv, mx, p.max_splits)
+                                                            : p.max_splits;
+    int c = (mx + s - 1) / s;
     c = max(kMinChunk, (c + 15) & ~15);
     chunk_s = c;
     p.meta[1] = c;
@@ -142,7 +230,7 @@ static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
     hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
     MSGL_CHECK_LAUNCH("msgl_paged_decode (plan)");
   }
-  hipLaunchKernelGGL((paged_decode_kernel<T, KV, D, G>), dim3(batch * p.max_splits * p.ngrp), dim3(64 * nwaves),
+  hipLaunchKernelGGL((paged_decode_kernel<T, KV, D, G>), dim3((unsigned)dec::decode_items(p)), dim3(64 * nwaves),
                      lds, stream, p);
   MSGL_CHECK_LAUNCH("msgl_paged_decode");
   if (p.max_splits > 1) {
@@ -153,16 +241,52 @@ static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
   return MSGL_OK;
 }
 
-template <typename T, typename KV, int D>
-static int dispatch_group(const DecodeParams& p, int batch, int group, hipStream_t stream) {
+struct Launch {
+  const DecodeParams& p;
+  int batch;
+  hipStream_t stream;
+  template <typename T, typename KV, int D, int G>
+  int run() const { return launch_decode<T, KV, D, G>(p, batch, stream); }
+};
+
+// Workgroups of paged_decode_kernel<T, KV, D, G> the device holds at once
+// (occupancy x CUs), measured once per process and shape.
+struct Resident {
+  int nwaves;
+  int* out;
+  bool* ranges;  // the instantiation has the key-range form
+  template <typename T, typename KV, int D, int G>
+  int run() const {
+    *ranges = decode_ranges<T, KV, D, G>();
+    static int cached[MSGL_DECODE_WAVES_PER_WG + 1] = {};
+    int& c = cached[nwaves];
+    if (c == 0) {
+      int per_cu = 0, dev = 0, cus = 0;
+      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &per_cu, reinterpret_cast<const void*>(&paged_decode_kernel<T, KV, D, G>), 64 * nwaves,
+              decode_lds_bytes<KV, D>(nwaves)) != hipSuccess ||
+          hipGetDevice(&dev) != hipSuccess ||
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
+        set_error("msgl_paged_decode: occupancy query failed: %s", hipGetErrorString(hipGetLastError()));
+        return MSGL_ERR_HIP;
+      }
+      c = per_cu * cus > 0 ? per_cu * cus : 1;
+    }
+    *out = c;
+    return MSGL_OK;
+  }
+};
+
+template <typename T, typename KV, int D, typename F>
+static int dispatch_group(const F& f, int group) {
   constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
   switch (group) {
-    case 1: return launch_decode<T, KV, D, 1>(p, batch, stream);
-    case 2: return launch_decode<T, KV, D, 2>(p, batch, stream);
-    case 4: return launch_decode<T, KV, D, 4>(p, batch, stream);
-    case 8: return launch_decode<T, KV, D, 8>(p, batch, stream);
+    case 1: return f.template run<T, KV, D, 1>();
+    case 2: return f.template run<T, KV, D, 2>();
+    case 4: return f.template run<T, KV, D, 4>();
+    case 8: return f.template run<T, KV, D, 8>();
     case 16:
-      if constexpr (!Q8) return launch_decode<T, KV, D, 16>(p, batch, stream);
+      if constexpr (!Q8) return f.template run<T, KV, D, 16>();
       [[fallthrough]];
     default:
       set_error("msgl_paged_decode: Hq/Hkv = %d not built (1, 2, 4, 8%s)", group, Q8 ? " for fp8 pools" : ", 16");
@@ -170,20 +294,40 @@ static int dispatch_group(const DecodeParams& p, int batch, int group, hipStream
   }
 }
 
-template <typename T, typename KV = T>
-static int dispatch_dim(const DecodeParams& p, int batch, int head_dim, int group, hipStream_t stream) {
+template <typename T, typename KV = T, typename F>
+static int dispatch_dim(const F& f, int head_dim, int group) {
   switch (head_dim) {
-    case 64: return dispatch_group<T, KV, 64>(p, batch, group, stream);
-    case 128: return dispatch_group<T, KV, 128>(p, batch, group, stream);
-    case 256: return dispatch_group<T, KV, 256>(p, batch, group, stream);
+    case 64: return dispatch_group<T, KV, 64>(f, group);
+    case 128: return dispatch_group<T, KV, 128>(f, group);
+    case 256: return dispatch_group<T, KV, 256>(f, group);
     default:
       set_error("msgl_paged_decode: head_dim %d not built (64, 128, 256)", head_dim);
       return MSGL_ERR_UNSUPPORTED;
   }
 }
 
+// The kernel instantiation of (dtype, fp8 pool, head_dim, group) applied to f.
+template <typename F>
+static int dispatch(const F& f, int dtype, bool q8, int head_dim, int group, const char* fn) {
+  if (q8) {  // fp8 e4m3 pools with per-(slot, kv head) scales
+    switch (dtype) {
+      case MSGL_BF16: return dispatch_dim<bf16_t, fp8e4m3>(f, head_dim, group);
+      case MSGL_F16: return dispatch_dim<f16_t, fp8e4m3>(f, head_dim, group);
+    }
+    set_error("%s: fp8 pools take bf16 or fp16 queries (dtype %d)", fn, dtype);
+    return MSGL_ERR_UNSUPPORTED;
+  }
+  switch (dtype) {
+    case MSGL_F32: return dispatch_dim<float>(f, head_dim, group);
+    case MSGL_BF16: return dispatch_dim<bf16_t>(f, head_dim, group);
+    case MSGL_F16: return dispatch_dim<f16_t>(f, head_dim, group);
+  }
+  set_error("%s: unknown dtype %d", fn, dtype);
+  return MSGL_ERR_UNSUPPORTED;
+}
+
 // Workspace layout, each region 256-byte aligned: [meta | plan B*S*ngrp int4 |
-// (S > 1) m,l B*S*Hq*2 f32 | acc B*S*Hq*D f32].
+// key offsets (B+1) i64 | (S > 1) m,l B*S*Hq*2 f32 | acc B*S*Hq*D f32].
 static inline int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 
 static inline int decode_groups(int hkv) {
@@ -192,37 +336,57 @@ static inline int decode_groups(int hkv) {
 }
 
 struct DecodeWorkspace {
-  int64_t plan, part_ml, part_o, bytes;
+  int64_t plan, tok_off, part_ml, part_o, bytes;
 };
 static inline DecodeWorkspace decode_workspace(int batch, int hq, int hkv, int head_dim, int splits) {
   DecodeWorkspace w;
   const int64_t units = splits > 1 ? (int64_t)batch * splits * hq : 0;
   w.plan = 256;
-  w.part_ml = w.plan + align256((int64_t)batch * splits * decode_groups(hkv) * 16);
+  w.tok_off = w.plan + align256((int64_t)batch * splits * decode_groups(hkv) * 16);
+  w.part_ml = w.tok_off + align256(((int64_t)batch + 1) * 8);
   w.part_o = w.part_ml + align256(units * 2 * 4);
   w.bytes = w.part_o + align256(units * head_dim * 4);
   return w;
 }
 
+// Key ranges of a balanced launch: one per workgroup the device holds at once,
+// per kv-head group.
+#ifndef MSGL_DECODE_RANGE_ROUNDS
+#define MSGL_DECODE_RANGE_ROUNDS 1
+#endif
+
+
 }  // namespace msgl
 
+int64_t msgl::dec::decode_items(const DecodeParams& p) {
+  // a balanced launch is chosen on the device (balanced_launch), so the grid
+  // covers both forms; workgroups past the chosen one's items exit at once
+  const int64_t list = (int64_t)p.batch * p.max_splits * p.ngrp;
+  return p.balanced ? std::max<int64_t>((int64_t)p.nranges * p.ngrp, list) : list;
+}
+
 extern "C" int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len) {
-  // Aim for ~4096 wavefronts (a bit over one round of MI355X at 3 waves/SIMD):
-  // enough units for ragged lengths to balance, few enough that the split-K
-  // partials and the merge stay small. No chunk is shorter than kMinChunk.
-  // Chunks of at most kMaxChunk tokens keep long-context batches balanced
-  // (the dispatcher needs more items than resident slots).
+  // max_splits bounds both split forms. Key ranges (one per resident
+  // workgroup, about 256 per kv-head group on MI355X) are at least
+  // ceil(max_b L_b / (max_splits - 1)) keys long: S = 2 + ceil(8192 / (B Hkv)),
+  // at least 4, leaves room for the longest request to be ~8x the average
+  // before its ranges must grow, and a request of max_seq_len keys overlaps at
+  // most ceil(max_seq_len / kMinChunk) + 1 ranges. Per-request chunks take the
+  // plan's chunk count (~4096 wavefronts, chunks of kMinChunk..2048 keys),
+  // which S must not cap.
   if (batch <= 0 || num_kv_heads <= 0) return 1;
-  constexpr int64_t kMaxChunk = 2048;
-  const int64_t target_waves = 4096;
-  int64_t s = (target_waves + (int64_t)batch * num_kv_heads - 1) / ((int64_t)batch * num_kv_heads);
+  const int64_t units = (int64_t)batch * num_kv_heads;
+  int64_t s = 2 + (8192 + units - 1) / units;
+  if (s < 4) s = 4;
+  int64_t c = (4096 + units - 1) / units;
   if (max_seq_len > 0) {
     const int64_t cap = (max_seq_len + msgl::kMinChunk - 1) / msgl::kMinChunk;
-    if (s > cap) s = cap;
-    const int64_t floor_s = (max_seq_len + kMaxChunk - 1) / kMaxChunk;
-    if (s < floor_s) s = floor_s;
+    if (s > cap + 1) s = cap + 1;
+    if (c > cap) c = cap;
+    const int64_t floor_c = (max_seq_len + 2047) / 2048;
+    if (c < floor_c) c = floor_c;
   }
-  if (s < 1) s = 1;
+  if (s < c) s = c;
   if (s > msgl::kMaxSplits) s = msgl::kMaxSplits;
   return (int32_t)s;
 }
@@ -281,6 +445,7 @@ extern "C" int msgl_paged_decode_plan(const int32_t* kv_indptr, const int32_t* s
   p.seq_lens = seq_lens;
   p.meta = reinterpret_cast<int*>(ws);
   p.plan = reinterpret_cast<int4*>(ws + w.plan);
+  p.tok_off = reinterpret_cast<int64_t*>(ws + w.tok_off);
   p.hq = num_qo_heads;
   p.hkv = num_kv_heads;
   p.max_splits = max_splits;
@@ -461,6 +626,7 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
   uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
   p.meta = reinterpret_cast<int*>(ws);
   p.plan = reinterpret_cast<int4*>(ws + w.plan);
+  p.tok_off = reinterpret_cast<int64_t*>(ws + w.tok_off);
   p.part_ml = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_ml) : nullptr;
   p.part_o = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_o) : nullptr;
   p.batch = batch;
@@ -472,6 +638,18 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
   p.page_size = page_size;
   p.max_splits = max_splits;
   p.scale_log2 = scale * kLog2e;
+  p.balanced = false;
+  p.nranges = 1;
+  if (max_splits > 1) {
+    const int nwaves = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
+    int resident = 0;
+    bool ranges = false;
+    const int st = dispatch(Resident{nwaves, &resident, &ranges}, dtype, kv_scale != nullptr, head_dim,
+                            num_qo_heads / num_kv_heads, fn);
+    if (st != MSGL_OK) return st;
+    p.balanced = ranges;
+    p.nranges = std::max(1, resident * MSGL_DECODE_RANGE_ROUNDS / p.ngrp);
+  }
   return MSGL_OK;
 }
 
@@ -490,20 +668,6 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
                                     page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, p,
                                     empty);
   if (st != MSGL_OK || empty) return st;
-  const int group = num_qo_heads / num_kv_heads;
-  hipStream_t s = (hipStream_t)stream;
-  if (kv_scale != nullptr) {  // fp8 e4m3 pools with per-(slot, kv head) scales
-    switch (dtype) {
-      case MSGL_BF16: return dispatch_dim<bf16_t, fp8e4m3>(p, batch, head_dim, group, s);
-      case MSGL_F16: return dispatch_dim<f16_t, fp8e4m3>(p, batch, head_dim, group, s);
-    }
-    set_error("%s: fp8 pools take bf16 or fp16 queries (dtype %d)", fn, dtype);
-    return MSGL_ERR_UNSUPPORTED;
-  }
-  switch (dtype) {
-    case MSGL_F32: return dispatch_dim<float>(p, batch, head_dim, group, s);
-    case MSGL_BF16: return dispatch_dim<bf16_t>(p, batch, head_dim, group, s);
-    case MSGL_F16: return dispatch_dim<f16_t>(p, batch, head_dim, group, s);
-  }
-  return MSGL_ERR_UNSUPPORTED;
+  return dispatch(Launch{p, batch, (hipStream_t)stream}, dtype, kv_scale != nullptr, head_dim,
+                  num_qo_heads / num_kv_heads, fn);
 }

@@ -37,19 +37,26 @@ def test_abi_version_and_sizes():
     lib = _lib.load()
     assert lib.msgl_abi_version() == 1
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
-    # [meta | work list: B x splits x kv-head groups (8 heads / 4 per workgroup) int4 | partials]
-    assert lib.msgl_paged_decode_workspace_size(128, 16, 8, 128, 1) == 256 + up(128 * 1 * 2 * 16)
+    # [meta | work list: B x splits x kv-head groups (8 heads / 4 per workgroup) int4 | key offsets (B + 1) i64 |
+    #  partials]
+    assert lib.msgl_paged_decode_workspace_size(128, 16, 8, 128, 1) == 256 + up(128 * 1 * 2 * 16) + up(129 * 8)
     ws = lib.msgl_paged_decode_workspace_size(128, 16, 8, 128, 16)
     units = 128 * 16 * 16
-    assert ws == 256 + up(128 * 16 * 2 * 16) + up(units * 8) + up(units * 128 * 4)
+    assert ws == 256 + up(128 * 16 * 2 * 16) + up(129 * 8) + up(units * 8) + up(units * 128 * 4)
     assert lib.msgl_paged_decode_workspace_size(1, 16, 8, 128, 1000) == lib.msgl_paged_decode_workspace_size(
         1, 16, 8, 128, 64)
-    assert 1 <= lib.msgl_paged_decode_default_splits(128, 8, 2048) <= 64
+    # splits bound the key ranges one request may overlap: 2 + ceil(8192 / (B Hkv)) in [4, 64], and no more
+    # than ranges of >= 64 keys can cut max_seq_len into (ceil(max_seq_len / 64) + 1); never below the
+    # per-request chunk count (~4096 wavefronts, chunks of at most 2048 keys)
+    assert lib.msgl_paged_decode_default_splits(128, 8, 32768) == 16
+    assert lib.msgl_paged_decode_default_splits(128, 8, 2048) == 10
+    assert lib.msgl_paged_decode_default_splits(128, 8, 0) == 10
     assert lib.msgl_paged_decode_default_splits(1, 8, 32768) == 64
-    assert lib.msgl_paged_decode_default_splits(128, 8, 2048) == 4
-    assert lib.msgl_paged_decode_default_splits(1, 8, 100) == 2  # capped by ceil(100 / 64)
-    assert lib.msgl_paged_decode_default_splits(128, 8, 32768) == 16  # chunks of at most 2048 tokens
-    assert lib.msgl_paged_decode_default_splits(256, 8, 8192) == 4
+    assert lib.msgl_paged_decode_default_splits(1, 8, 100) == 3
+    assert lib.msgl_paged_decode_default_splits(1, 8, 64) == 2
+    assert lib.msgl_paged_decode_default_splits(256, 8, 8192) == 6
+    assert lib.msgl_paged_decode_default_splits(4096, 8, 8192) == 4
+    assert lib.msgl_paged_decode_default_splits(0, 8, 8192) == 1
 
 
 def test_prefill_sizes():

@@ -192,6 +192,42 @@ def test_cfg3_long_contexts_page16(cuda_device):
     assert_close(out[pick], ref, dt, "cfg3 sampled")
 
 
+def test_key_ranges_long_contexts_page16(cuda_device):
+    """~1.2M keys (Qwen3-8B heads, page 16, contexts 4096..8192): enough keys for the
+    launch to split by equal key ranges of the batch's token stream (>= 2048 keys per
+    range even at 4 resident workgroups per CU). Sampled requests vs the oracle; the
+    fused store and a reused plan give the same bits as the separate calls."""
+    batch = 200
+    c = workloads.decode_case(batch, 4096, 8192, 1 << 21, 16, seed=3)
+    cus = torch.cuda.get_device_properties(cuda_device).multi_processor_count
+    assert int(c.lens.sum()) >= 2048 * 4 * cus // 2, "too few keys to select key ranges"
+    dt = torch.bfloat16
+    kp, vp = _pools(1 << 21, 8, 128, dt, 820, cuda_device)
+    q = randn((batch, 32, 128), 822, dt).to(cuda_device)
+    kn = randn((batch, 8, 128), 823, dt).to(cuda_device)
+    vn = randn((batch, 8, 128), 824, dt).to(cuda_device)
+    indptr, pages, lens = i32(c.page_indptr, cuda_device), i32(c.page_ids, cuda_device), i32(c.lens, cuda_device)
+    loc = i32(c.out_loc, cuda_device)
+    kp2, vp2 = kp.clone(), vp.clone()
+    print("case key-ranges 8B page16", flush=True)
+    kw = dict(seq_lens=lens, page_size=16)
+    out = ops.paged_decode_attention(q, kp, vp, indptr, pages, 128**-0.5, new_kv=(kn, vn, loc), **kw)
+    ops.store_kv(kn, vn, loc, kp2, vp2)
+    ref_out = ops.paged_decode_attention(q, kp2, vp2, indptr, pages, 128**-0.5, **kw)
+    splits = ops.default_splits(batch, 8, int(c.lens.max()))
+    ws = ops.decode_workspace(batch, 32, 8, 128, splits, cuda_device)
+    ops.paged_decode_plan(indptr, lens, batch, 32, 8, 128, splits, ws)
+    planned = ops.paged_decode_attention(q, kp2, vp2, indptr, pages, 128**-0.5, max_splits=splits, workspace=ws,
+                                         planned=True, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(kp.view(torch.int16), kp2.view(torch.int16))
+    assert torch.equal(out, ref_out), "fused store != store + decode"
+    assert torch.equal(planned, ref_out), "planned != unplanned"
+    pick = [0, 1, 57, 99, 100, 150, 198, 199]
+    ref = _sampled_ref(q, kp2, vp2, c, pick, 128**-0.5, page_size=16)
+    assert_close(out[pick], ref, dt, "key ranges sampled")
+
+
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
 @pytest.mark.parametrize("splits", [1, 4])
 def test_fused_store_matches_two_calls(cuda_device, dtype, splits):

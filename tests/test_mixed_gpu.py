@@ -111,7 +111,12 @@ def test_mixed_step_full_size(cuda_device):
     torch.cuda.synchronize()
     assert torch.equal(out, out2), "mixed step is not deterministic"
     assert torch.equal(out, out3), "the two-stream step differs from the one-stream order"
-    assert torch.equal(out, out4), "the single-launch step differs from the one-stream order"
+    # The decode call alone splits this batch (2.2M keys) by equal key ranges; the
+    # single launch runs per-request chunks, so the two agree to rounding, not bits
+    # (the prefill rows are the same bits).
+    np_dec = case.num_decode  # decode rows come first in the packed batch
+    assert torch.equal(out[np_dec:], out4[np_dec:]), "single-launch prefill rows differ"
+    assert_close(out4[:np_dec], to_np64(out[:np_dec]), dt, "single launch vs decode call")
     longest = int(np.argmax(case.device_len[: case.num_decode]))
     for i in sorted({0, 5, longest, case.num_decode - 1}):
         _check_request(case, i, q, kp, vp, out)
