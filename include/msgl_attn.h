@@ -75,14 +75,16 @@ int msgl_store_kv(const void* k, const void* v, const int32_t* out_loc, void* k_
                   int64_t num_tokens, int32_t num_kv_heads, int32_t head_dim, int64_t num_slots,
                   int32_t dtype, void* stream);
 
-/* Default split count for msgl_paged_decode (max_splits <= 0 picks this). */
+/* Default split count for msgl_paged_decode (max_splits <= 0 picks this);
+ * max_seq_len (0: unknown) caps it at what a request of that length can use. */
 int32_t msgl_paged_decode_default_splits(int32_t batch, int32_t num_kv_heads, int32_t max_seq_len);
 
 /*
- * Bytes of workspace msgl_paged_decode needs for these sizes (0 when
- * max_splits <= 1): fp32 split-K partials (m, l and the unnormalised output
- * per chunk and query head). Its contents need no initialisation. Calls that
- * overlap in time must not share a workspace; calls in order on one stream may.
+ * Bytes of workspace msgl_paged_decode needs for these sizes: the plan (work
+ * list and per-request key offsets) and, when max_splits > 1, fp32 split-K
+ * partials (m, l and the unnormalised output per chunk and query head). Its
+ * contents need no initialisation. Calls that overlap in time must not share a
+ * workspace; calls in order on one stream may.
  */
 int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads,
                                          int32_t head_dim, int32_t max_splits);
@@ -101,7 +103,10 @@ int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, in
  *   seq_lens   [B] tokens per request, or NULL (then L_b = indptr[b+1]-indptr[b],
  *              page_size must be 1)
  *   scale      softmax scale (attention/base.py:45: head_dim ** -0.5)
- *   max_splits split-K factor bound (<= 0: msgl_paged_decode_default_splits)
+ *   max_splits split-K bound (<= 0: msgl_paged_decode_default_splits): the most
+ *              partials one request's keys are cut into, whether by per-request
+ *              chunks or (long-context batches) by equal key ranges of the
+ *              batch's concatenated keys
  *   out        [B, Hq, D]
  *   workspace  >= msgl_paged_decode_workspace_size(B, Hq, Hkv, D, max_splits)
  *              bytes, 256-byte aligned
