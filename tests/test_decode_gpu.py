@@ -5,6 +5,8 @@ cases are BASELINE's decode workloads (checked on sampled requests, plus
 size-independent properties at full size).
 """
 
+import types
+
 import numpy as np
 import pytest
 import torch
@@ -226,6 +228,39 @@ def test_key_ranges_long_contexts_page16(cuda_device):
     pick = [0, 1, 57, 99, 100, 150, 198, 199]
     ref = _sampled_ref(q, kp2, vp2, c, pick, 128**-0.5, page_size=16)
     assert_close(out[pick], ref, dt, "key ranges sampled")
+
+
+def test_key_ranges_ragged_extremes(cuda_device):
+    """Key ranges over a batch with empty requests, one- and few-key requests between
+    them and two requests of 400k / 350k keys (the range length is then set by the
+    longest request, ceil(400000 / (S - 1))): zero rows for L = 0, the long requests
+    agree with the unsplit decode (one workgroup per request), the short ones with
+    the oracle."""
+    rng = np.random.default_rng(11)
+    lens = rng.integers(0, 4000, size=64).astype(np.int32)
+    lens[[0, 5, 6, 40, 63]] = 0
+    lens[[1, 7, 41]] = [1, 2, 17]
+    lens[3], lens[50] = 400000, 350000
+    n = int(lens.sum())
+    cus = torch.cuda.get_device_properties(cuda_device).multi_processor_count
+    assert n >= 2048 * 3 * cus // 2, "too few keys to select key ranges"
+    indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
+    indices = rng.permutation(1 << 21)[:n].astype(np.int32)
+    dt = torch.bfloat16
+    kp, vp = _pools(1 << 21, 8, 128, dt, 830, cuda_device)
+    q = randn((64, 16, 128), 832, dt).to(cuda_device)
+    ip, ix = i32(indptr, cuda_device), i32(indices, cuda_device)
+    print("case key-ranges ragged extremes", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, ip, ix, 128**-0.5, max_seq_len=int(lens.max()))
+    one = ops.paged_decode_attention(q, kp, vp, ip, ix, 128**-0.5, max_splits=1)
+    torch.cuda.synchronize()
+    zero = [i for i in range(64) if lens[i] == 0]
+    assert torch.count_nonzero(out[zero]) == 0
+    assert_close(out[[3, 50]], to_np64(one[[3, 50]]), dt, "long requests vs unsplit")
+    short = [1, 2, 7, 41, 42, 62]
+    case = types.SimpleNamespace(kv_indptr=indptr, kv_indices=indices)
+    ref = _sampled_ref(q, kp, vp, case, short, 128**-0.5)
+    assert_close(out[short], ref, dt, "short requests vs oracle")
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16"])
