@@ -136,7 +136,8 @@ struct DecodeParams {
   void* k_pool_w;
   void* v_pool_w;
   // work list (plan kernel output, in the workspace)
-  int* meta;        // [0] items in the plan, [1] batch-wide chunk length, [3] max_b L_b
+  int* meta;        // [0] items in the plan, [1] batch-wide chunk length, [2] the plan's max_splits
+                    // (with key offsets), [3] max_b L_b
   int4* plan;       // (request, split, kv-head group, 0), longest first
   int64_t* tok_off; // balanced split: [B+1] tokens of the requests before b (tok_off[B] = all)
   int nranges;      // balanced split: key ranges of the launch (grid / ngrp)
@@ -147,12 +148,13 @@ struct DecodeParams {
   float scale_log2;
 };
 
-// Whether this launch splits by equal key ranges: allowed, and the batch's
-// keys (tok_off[B], from the plan) average at least
-// MSGL_DECODE_BALANCED_MIN_RANGE per range. Used identically by the decode and
-// merge kernels; otherwise both follow the per-request work list.
+// Whether this launch splits by equal key ranges: allowed, the plan wrote key
+// offsets for this max_splits, and the batch's keys (tok_off[B]) average at
+// least MSGL_DECODE_BALANCED_MIN_RANGE per range. Used identically by the
+// decode and merge kernels; otherwise both follow the per-request work list.
 __device__ __forceinline__ bool balanced_launch(const DecodeParams& p) {
-  return p.balanced && p.tok_off[p.batch] >= (int64_t)MSGL_DECODE_BALANCED_MIN_RANGE * p.nranges;
+  return p.balanced && p.meta[2] == p.max_splits &&
+         p.tok_off[p.batch] >= (int64_t)MSGL_DECODE_BALANCED_MIN_RANGE * p.nranges;
 }
 
 // LDS per wavefront: P tile [16 tokens][16 rows] + alpha[16] + (m, l)[16 rows].

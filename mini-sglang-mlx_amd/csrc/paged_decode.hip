@@ -167,6 +167,7 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeP
       int m = 0;
       for (int w = 0; w < kPlanThreads / 64; ++w) m = max(m, wmax[w]);
       p.meta[3] = m;
+      p.meta[2] = p.max_splits;  // key offsets written for this bound
     }
     __syncthreads();  // wmax is reused below
   }
@@ -185,6 +186,7 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeP
   for (int i = threadIdx.x; i < 256; i += kPlanThreads) hist[i] = 0;
   __syncthreads();
   if (threadIdx.x == 0) {
+    if (p.max_splits <= 1) p.meta[2] = 0;  // no key offsets
     int mx = 0;
     for (int w = 0; w < kPlanThreads / 64; ++w) mx = max(mx, wmax[w]);
     const int s = MSGL_DECODE_BALANCED && p.max_splits > 1 ? chunk_splits(p.batch, p.hkv, mx, p.max_splits)
