@@ -181,6 +181,15 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 // (The 16x16x32 form runs at half this rate on gfx950.)
 template <typename T>
 struct MMA32;
+
+// Wave priority (s_setprio) of a wavefront in its P.V block (the P.V MFMAs
+// with the next tile's exp/pack between them) over one in its S block: 1 raised
+// for the S block instead, 0 none. With the P.V block raised the fp8 prefill
+// ran 88.5 -> 81.5 us per layer and the bf16 one 73.6 -> 73.1 (the S block
+// raised: 81.8 / 73.5; each MFMA's issue raised: 83.2 / 74.4).
+#ifndef MSGL_PREFILL_SETPRIO
+#define MSGL_PREFILL_SETPRIO 2
+#endif
 template <>
 struct MMA32<bf16_t> {
   __device__ __forceinline__ static f32x16 mma(const u32x4& a, const u32x4& b, const f32x16& c) {
@@ -435,6 +444,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
     k_read(st, ko);
     float m = -INFINITY;
     f32x16 acc_s = {};
+    if (MSGL_PREFILL_SETPRIO == 1) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int j = 0; j < NQF; ++j) {
       acc_s = MMA32<T>::mma(k_operand(ko, j), qf[j], acc_s);
@@ -448,6 +458,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    if (MSGL_PREFILL_SETPRIO == 1) __builtin_amdgcn_s_setprio(0);
     sdst = acc_s;
     return m;
   };
@@ -532,6 +543,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
   auto pv_probs = [&](int st, const u32x4 (&pa)[2], const float (&x)[16], const float (&vs)[16],
                       u32x4 (&pa_new)[2], auto do_pv) {
     constexpr bool DO_PV = decltype(do_pv)::value;
+    if (MSGL_PREFILL_SETPRIO == 2) __builtin_amdgcn_s_setprio(1);
     constexpr int NMF = 2 * NDT;
     constexpr int EPM = 16 / NMF;
     const uint8_t* Vb = smem + st * Geo::STAGE_BYTES + Geo::TILE_BYTES;
@@ -595,6 +607,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       __builtin_amdgcn_sched_barrier(0);
     }
     l_run += Q8 ? ls[0] + ls[1] : lp;
+    if (MSGL_PREFILL_SETPRIO == 2) __builtin_amdgcn_s_setprio(0);
   };
   // Software pipeline per window, three tiles deep. Iteration t:
   //   A: the S MFMAs of tile t+1 interleaved with tile t's masked row max;
