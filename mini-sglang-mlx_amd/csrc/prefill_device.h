@@ -182,13 +182,19 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 template <typename T>
 struct MMA32;
 
-// Wave priority (s_setprio) of a wavefront in its P.V block (the P.V MFMAs
-// with the next tile's exp/pack between them) over one in its S block: 1 raised
-// for the S block instead, 0 none. With the P.V block raised the fp8 prefill
-// ran 88.5 -> 81.5 us per layer and the bf16 one 73.6 -> 73.1 (the S block
-// raised: 81.8 / 73.5; each MFMA's issue raised: 83.2 / 74.4).
+// Wave priorities (s_setprio) inside the key loop, so that of the two
+// wavefronts of a SIMD the one issuing a tile's LDS transfers goes first, then
+// the one in its P.V block (the P.V MFMAs with the next tile's exp/pack between
+// them), then the one in its S block. Measured on the 16-request workload
+// (same box, alternating runs; no priorities: bf16 73.6, fp8 88.5 us/layer):
+//   P.V 1:                 bf16 73.2, fp8 80.9
+//   S 1, P.V 2:            bf16 73.0, fp8 80.4
+//   P.V 1, transfers 3:    bf16 71.9, fp8 80.8   (bf16 pools)
+//   S 1, P.V 2, transfers 3: bf16 72.6, fp8 79.9 (fp8 pools)
+//   each MFMA's issue 1:   bf16 74.4, fp8 83.2
+// 0 turns them off.
 #ifndef MSGL_PREFILL_SETPRIO
-#define MSGL_PREFILL_SETPRIO 2
+#define MSGL_PREFILL_SETPRIO 1
 #endif
 template <>
 struct MMA32<bf16_t> {
@@ -444,7 +450,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
     k_read(st, ko);
     float m = -INFINITY;
     f32x16 acc_s = {};
-    if (MSGL_PREFILL_SETPRIO == 1) __builtin_amdgcn_s_setprio(1);
+    if (MSGL_PREFILL_SETPRIO && Q8) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int j = 0; j < NQF; ++j) {
       acc_s = MMA32<T>::mma(k_operand(ko, j), qf[j], acc_s);
@@ -458,7 +464,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if (MSGL_PREFILL_SETPRIO == 1) __builtin_amdgcn_s_setprio(0);
+    if (MSGL_PREFILL_SETPRIO && Q8) __builtin_amdgcn_s_setprio(0);
     sdst = acc_s;
     return m;
   };
@@ -543,7 +549,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
   auto pv_probs = [&](int st, const u32x4 (&pa)[2], const float (&x)[16], const float (&vs)[16],
                       u32x4 (&pa_new)[2], auto do_pv) {
     constexpr bool DO_PV = decltype(do_pv)::value;
-    if (MSGL_PREFILL_SETPRIO == 2) __builtin_amdgcn_s_setprio(1);
+    if (MSGL_PREFILL_SETPRIO) __builtin_amdgcn_s_setprio(Q8 ? 2 : 1);
     constexpr int NMF = 2 * NDT;
     constexpr int EPM = 16 / NMF;
     const uint8_t* Vb = smem + st * Geo::STAGE_BYTES + Geo::TILE_BYTES;
@@ -607,7 +613,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       __builtin_amdgcn_sched_barrier(0);
     }
     l_run += Q8 ? ls[0] + ls[1] : lp;
-    if (MSGL_PREFILL_SETPRIO == 2) __builtin_amdgcn_s_setprio(0);
+    if (MSGL_PREFILL_SETPRIO) __builtin_amdgcn_s_setprio(0);
   };
   // Software pipeline per window, three tiles deep. Iteration t:
   //   A: the S MFMAs of tile t+1 interleaved with tile t's masked row max;
@@ -675,7 +681,9 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       const int stp = SC >= 0 ? (SC + NS - 1) % NS : (t + NS - 1) % NS;
       if (t + 1 < ntiles) vm_wait<0>();  // tile t+1, the only one in flight, landed
       __syncthreads();  // tile t+1 visible; everyone is done with tile t-2's stage
+      if (MSGL_PREFILL_SETPRIO) __builtin_amdgcn_s_setprio(3);
       if (t + 2 < ntiles) issue(st2);
+      if (MSGL_PREFILL_SETPRIO) __builtin_amdgcn_s_setprio(0);
       const int kbase = w0 + t * KT;
       // A (past the last tile, scores reads a stage whose transfers have all landed; unused)
       f32x16 s_next;
