@@ -193,6 +193,9 @@ struct MMA32;
 //   S 1, P.V 2, transfers 3: bf16 72.6, fp8 79.9 (fp8 pools)
 //   each MFMA's issue 1:   bf16 74.4, fp8 83.2
 // 0 turns them off.
+#ifndef MSGL_PREFILL_SKIP_DEAD
+#define MSGL_PREFILL_SKIP_DEAD 1
+#endif
 #ifndef MSGL_PREFILL_SETPRIO
 #define MSGL_PREFILL_SETPRIO 1
 #endif
@@ -308,6 +311,10 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
   // this lane's query row, clamped into range so every row sees key 0; rows
   // past E are computed, not stored
   const int my_row = wave * 32 + rl;
+  // A wavefront whose 32 rows all lie past the extend (the last query block of
+  // a request) only moves tiles: it issues its share of the LDS transfers and
+  // meets every barrier, but computes nothing.
+  const bool live = !MSGL_PREFILL_SKIP_DEAD || qb + wave * 32 / G < E;
   const int my_tok = min(qb + my_row / G, E - 1);
   const int limit = P + my_tok;
   const int lim_lo = __builtin_amdgcn_readfirstlane(limit);  // the wavefront's first row (lane 0)
@@ -666,7 +673,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
     wait_tile(min(1, ntiles - 1));
     __syncthreads();  // tile 0 visible to all
     f32x16 s_cur;
-    scores(0, s_cur);
+    if (live) scores(0, s_cur);
     u32x4 pa_prev[2];
 
     // stc: tile t's ring stage as a compile-time constant (the main loop runs
@@ -690,6 +697,10 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       float x[16];
       float ksc[16];  // fp8: tile t's K scales
       if constexpr (Q8) tile_scales(st, 0, ksc);
+      if (!live) {
+        load_slots(t + 3, nw);
+        return;
+      }
       float mloc;
       if (kbase + KT <= kend && kbase + KT - 1 <= lim_lo) {
         mloc = scores_rowmax(st1, s_next, s_cur, ksc, x, 0, std::false_type{});
@@ -726,7 +737,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       }
     }
     for (; t < ntiles; ++t) iteration(t, std::false_type{}, std::integral_constant<int, -1>{});
-    pv((ntiles - 1) % NS, pa_prev);
+    if (live) pv((ntiles - 1) % NS, pa_prev);
   }
 
   // ---- results: accumulator i is WG row wave*32 + 8(i/4) + 4h + i%4, column 32dt + rl ----
