@@ -5,11 +5,12 @@
 //   o[b, h] = softmax_j(scale * q[b,h] . K[slot_b(j), h/G]) V[slot_b(j), h/G],  j < L_b
 //
 // Design (MI355X-first, not a translation of the Metal kernel):
-//  * Work unit = one wavefront per (request b, split s, kv head). Workgroups
-//    are small (one wavefront by default) so a CU refills as soon as any unit
-//    finishes; the kv heads of one (b, s) are neighbouring workgroups, so the
-//    rows of a slot (Hkv * D contiguous elements) are read close in time. A
-//    workgroup gathers its token slots once into LDS.
+//  * Work unit = one wavefront per (request b, split s, kv head); a workgroup
+//    holds the MSGL_DECODE_WAVES_PER_WG (4) neighbouring kv heads of one
+//    (b, s) -- measured faster than 1 or 2 -- and the kv-head groups of a
+//    (b, s) are neighbouring workgroups, so the rows of a slot (Hkv * D
+//    contiguous elements) are read close in time. A workgroup gathers its
+//    token slots once into LDS.
 //  * Split-K, two forms. Per-request chunks: every request is cut into chunks
 //    of one batch-wide length, ceil(max_b L_b / s) rounded to 16 tokens
 //    (>= kMinChunk), and a one-workgroup plan kernel lists the (request,
