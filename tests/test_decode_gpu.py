@@ -1,7 +1,7 @@
 """Paged decode on the GPU vs the float64 oracle (attention/naive.py:50-60 semantics).
 
 Shape grid and edge lengths follow tests/test_attention.py:19-39; the larger
-cases are BASELINE's decode workloads (checked on sampled requests, plus
+cases are the benchmark's decode workloads (checked on sampled requests, plus
 size-independent properties at full size).
 """
 
