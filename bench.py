@@ -95,12 +95,12 @@ def cpu_baseline(seconds: float):
         info = threadpoolctl.threadpool_info()
         threads = max([i.get("num_threads", 1) for i in info] or [1])
         cases = {
-            "cfg1": (workloads.decode_case(8, 100, 1024, 16384, 1, seed=0), 16384),
-            "cfg2_sample16": (workloads.decode_case(BATCH, LO, HI, POOL, 1, seed=0), POOL),
+            "batch8_ctx1k": (workloads.decode_case(8, 100, 1024, 16384, 1, seed=0), 16384),
+            "batch128_sample16": (workloads.decode_case(BATCH, LO, HI, POOL, 1, seed=0), POOL),
         }
         for name, (c, n) in cases.items():
             rng = np.random.default_rng(1)
-            b = 8 if name == "cfg1" else 16
+            b = 8 if name == "batch8_ctx1k" else 16
             lens = c.lens[:b]
             # random values tiled over the pool (the timing does not depend on them)
             block = rng.standard_normal(1 << 22, dtype=np.float32)
@@ -219,20 +219,20 @@ def bench_decode(args, dev):
     if not args.no_cpu:
         res, threads = cpu_baseline(args.cpu_seconds)
         cpu = {
-            "value": round(res["cfg1"]["gbs"], 3),
+            "value": round(res["batch8_ctx1k"]["gbs"], 3),
             "unit": "GB/s",
             "cores": threads,
             "kind": "port",
             "sample": (
                 "numpy fp32 restatement of the naive backend (attention/naive.py:36-60: padded gather, mask, "
-                f"softmax attention), best of {res['cfg1']['runs']} runs on the CPU reference config "
-                f"(B=8, L~U[100,1024] seed 0, ΣL={res['cfg1']['sum_len']}, pool 16384, 16q/8kv/128); "
-                f"{res['cfg1']['us_per_layer']:.0f} µs/layer. Same code on the first 16 requests of the "
-                f"benchmark batch (bf16 values as fp32, ΣL={res['cfg2_sample16']['sum_len']}): "
-                f"{res['cfg2_sample16']['us_per_layer']:.0f} µs/layer = {res['cfg2_sample16']['gbs']:.2f} GB/s"
+                f"softmax attention), best of {res['batch8_ctx1k']['runs']} runs on the CPU reference config "
+                f"(B=8, L~U[100,1024] seed 0, ΣL={res['batch8_ctx1k']['sum_len']}, pool 16384, 16q/8kv/128); "
+                f"{res['batch8_ctx1k']['us_per_layer']:.0f} µs/layer. Same code on the first 16 requests of the "
+                f"benchmark batch (bf16 values as fp32, ΣL={res['batch128_sample16']['sum_len']}): "
+                f"{res['batch128_sample16']['us_per_layer']:.0f} µs/layer = {res['batch128_sample16']['gbs']:.2f} GB/s"
             ),
-            "us_per_layer": round(res["cfg1"]["us_per_layer"], 1),
-            "cfg2_sample16_gbs": round(res["cfg2_sample16"]["gbs"], 3),
+            "us_per_layer": round(res["batch8_ctx1k"]["us_per_layer"], 1),
+            "batch128_sample16_gbs": round(res["batch128_sample16"]["gbs"], 3),
         }
 
     line = {

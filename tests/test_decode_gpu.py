@@ -120,18 +120,18 @@ def test_zero_length_request_gives_zeros(cuda_device):
         assert_close(out[[0, 2]], ref, dt, "zero-length neighbours")
 
 
-def test_cfg1_fp32_full(cuda_device):
+def test_batch8_ctx1k_fp32_full(cuda_device):
     """B=8, L ~ U[100,1024], pool 16384, page 1, fp32: every request vs the oracle at 1e-5."""
     c = workloads.decode_case(8, 100, 1024, 16384, 1, seed=0)
     dt = torch.float32
     kp, vp = _pools(16384, 8, 128, dt, 600, cuda_device)
     q = randn((8, 16, 128), 602, dt).to(cuda_device)
-    print("case cfg1", flush=True)
+    print("case batch8 ctx1k fp32", flush=True)
     out = ops.paged_decode_attention(q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device),
                                      128**-0.5)
     torch.cuda.synchronize()
     ref = oracle.paged_decode(to_np64(q), to_np64(kp), to_np64(vp), c.kv_indptr, c.kv_indices, 128**-0.5)
-    assert_close(out, ref, dt, "cfg1")
+    assert_close(out, ref, dt, "batch8 ctx1k")
 
 
 def _sampled_ref(q, kp, vp, c, pick, scale, page_size=1):
@@ -150,7 +150,7 @@ def _sampled_ref(q, kp, vp, c, pick, scale, page_size=1):
     return np.stack(outs)
 
 
-def test_cfg2_full_size(cuda_device):
+def test_batch128_ctx2k_full_size(cuda_device):
     """Batch 128, L ~ U[200,2048], pool 262144, bf16: sampled requests vs oracle, plus
     bitwise invariance under relocation of the KV rows and run-to-run determinism."""
     c = workloads.decode_case(128, 200, 2048, 262144, 1, seed=0)
@@ -158,14 +158,14 @@ def test_cfg2_full_size(cuda_device):
     kp, vp = _pools(262144, 8, 128, dt, 700, cuda_device)
     q = randn((128, 16, 128), 702, dt).to(cuda_device)
     indptr, indices = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
-    print("case cfg2", flush=True)
+    print("case batch128 ctx2k", flush=True)
     out = ops.paged_decode_attention(q, kp, vp, indptr, indices, 128**-0.5)
     out2 = ops.paged_decode_attention(q, kp, vp, indptr, indices, 128**-0.5)
     torch.cuda.synchronize()
     assert torch.equal(out, out2), "decode is not deterministic"
     pick = [0, 1, 17, 63, 64, 100, 126, 127]
     ref = _sampled_ref(q, kp, vp, c, pick, 128**-0.5)
-    assert_close(out[pick], ref, dt, "cfg2 sampled")
+    assert_close(out[pick], ref, dt, "batch128 ctx2k sampled")
     # relocate every used row to a new slot (a fixed permutation of the pool): same bits out
     perm = torch.from_numpy(np.random.default_rng(5).permutation(262144).astype(np.int64)).to(cuda_device)
     kp2 = torch.empty_like(kp)
@@ -177,13 +177,13 @@ def test_cfg2_full_size(cuda_device):
     assert torch.equal(out, out3), "result depends on where the rows live"
 
 
-def test_cfg3_long_contexts_page16(cuda_device):
+def test_8b_heads_long_contexts_page16(cuda_device):
     """Qwen3-8B heads (32/8/128), page 16, contexts 1024..8192 (reduced batch), split-K + merge."""
     c = workloads.decode_case(24, 1024, 8192, 1 << 20, 16, seed=0)
     dt = torch.bfloat16
     kp, vp = _pools(1 << 20, 8, 128, dt, 800, cuda_device)
     q = randn((24, 32, 128), 802, dt).to(cuda_device)
-    print("case cfg3-reduced", flush=True)
+    print("case 8b heads ctx8k page16", flush=True)
     out = ops.paged_decode_attention(
         q, kp, vp, i32(c.page_indptr, cuda_device), i32(c.page_ids, cuda_device), 128**-0.5,
         seq_lens=i32(c.lens, cuda_device), page_size=16,
@@ -191,7 +191,7 @@ def test_cfg3_long_contexts_page16(cuda_device):
     torch.cuda.synchronize()
     pick = list(range(0, 24, 3))
     ref = _sampled_ref(q, kp, vp, c, pick, 128**-0.5, page_size=16)
-    assert_close(out[pick], ref, dt, "cfg3 sampled")
+    assert_close(out[pick], ref, dt, "8b heads ctx8k sampled")
 
 
 def test_key_ranges_long_contexts_page16(cuda_device):

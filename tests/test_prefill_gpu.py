@@ -79,15 +79,15 @@ def test_prefill_page_size_16(cuda_device, dtype):
     assert_close(out, ref, dt, f"prefill page16 {dtype}")
 
 
-def test_prefill_cfg4_sampled(cuda_device):
+def test_prefill_16req_sampled(cuda_device):
     """16 requests, P ~ U[0,4096], E ~ U[64,512] rescaled to <= 2048 packed tokens, bf16."""
     case = workloads.prefill_case(16, 4096, 64, 512, 2048, num_slots=1 << 17, seed=0)
-    print("case prefill cfg4", flush=True)
+    print("case prefill 16 requests", flush=True)
     q, kn, vn, kp, vp, out = _run(case, 16, 8, 128, torch.bfloat16, cuda_device, 30)
     rows = [0, 3, 7, 15]
     ref = _oracle(case, q, kn, vn, kp, vp, 128, rows=rows)
     sel = np.concatenate([np.arange(case.q_indptr[i], case.q_indptr[i + 1]) for i in rows])
-    assert_close(out[torch.from_numpy(sel).to(cuda_device)], ref, torch.bfloat16, "cfg4 sampled")
+    assert_close(out[torch.from_numpy(sel).to(cuda_device)], ref, torch.bfloat16, "prefill 16 requests sampled")
     out2 = ops.prefill_ragged_attention(
         q, kp, vp, i32(case.q_indptr, cuda_device), i32(case.kv_indptr, cuda_device),
         i32(case.kv_indices, cuda_device), None, 128**-0.5, max_extend_len=int(case.extend_lens.max()),
