@@ -1,6 +1,6 @@
 """CPU oracle for the mini-sglang-mlx attention hot path.
 
-TEST INFRASTRUCTURE ONLY. This package is the checker, never the product:
+TEST INFRASTRUCTURE ONLY. This package checks results and is never the product:
 only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
 ``bench.py`` may import it. The HIP backend under ``mini-sglang-mlx_amd/`` never
 imports it and has no CPU fallback.
