@@ -129,7 +129,7 @@ def cpu_baseline(seconds: float):
 def main():
     args = parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        print("bench.py measures one GPU: the attention path has no cross-GPU work in this build "
+        print("bench.py measures one GPU: the attention path has no cross-GPU work "
               "(multi-GPU sharding is a design note only); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
 
@@ -653,7 +653,7 @@ def bench_mixed(args, dev):
 
 
 def bench_ceilings(args, dev):
-    """The box's own ceilings next to the spec peaks: a 1 GiB device-to-device
+    """The device's own ceilings next to the spec peaks: a 1 GiB device-to-device
     copy (HBM read + write) and an 8192^3 bf16 GEMM (hipBLASLt via torch)."""
     import torch
 

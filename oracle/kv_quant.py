@@ -3,7 +3,7 @@
 The reference names this extension without code (docs/09-exercises.md:81-82:
 store the KV pool as int8 / fp8 with one scale per token and head, and change
 ``store_kv`` (kvcache/pool.py:47-50) and the paged decode kernel accordingly).
-This build fixes the format as follows, and the oracle restates it:
+The library fixes the format as follows, and the oracle restates it:
 
 - element format: OCP fp8 e4m3 ("e4m3fn": bias 7, 3 mantissa bits, no
   infinities, largest finite 448, S.1111.111 is NaN), round to nearest even;
