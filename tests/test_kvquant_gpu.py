@@ -136,6 +136,35 @@ def test_fp8_planned_matches_unplanned(cuda_device):
     assert torch.equal(a, b)
 
 
+def test_fp8_key_ranges_long_contexts(cuda_device):
+    """~1M keys over fp8 pools (Qwen3-0.6B heads): enough for the decode launch to
+    split by equal key ranges. The fused quantising store gives the same bits as
+    store + decode, and the result agrees with the unsplit decode (one workgroup
+    per request and kv-head group)."""
+    b, hq, hkv, d = 160, 16, 8, 128
+    c = workloads.decode_case(b, 4096, 8192, 1 << 21, 1, seed=13)
+    cus = torch.cuda.get_device_properties(cuda_device).multi_processor_count
+    assert int(c.lens.sum()) >= 2048 * 3 * cus // 2, "too few keys to select key ranges"
+    n = 1 << 21
+    kp, vp, sc, _, _ = _fp8_pools(n, hkv, d, 410, cuda_device, spread=1.0)
+    kp2, vp2, sc2 = kp.clone(), vp.clone(), sc.clone()
+    q = randn((b, hq, d), 411, torch.bfloat16).to(cuda_device)
+    k_new = randn((b, hkv, d), 412, torch.bfloat16).to(cuda_device)
+    v_new = randn((b, hkv, d), 413, torch.bfloat16).to(cuda_device)
+    out_loc = i32(c.out_loc, cuda_device)
+    ip, ix = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    print("case fp8 key ranges", flush=True)
+    ops.store_kv_fp8(k_new, v_new, out_loc, kp, vp, sc)
+    a = ops.paged_decode_attention(q, kp, vp, ip, ix, d**-0.5, kv_scale=sc, max_seq_len=int(c.lens.max()))
+    f = ops.paged_decode_attention(q, kp2, vp2, ip, ix, d**-0.5, kv_scale=sc2, new_kv=(k_new, v_new, out_loc),
+                                   max_seq_len=int(c.lens.max()))
+    one = ops.paged_decode_attention(q, kp, vp, ip, ix, d**-0.5, kv_scale=sc, max_splits=1)
+    torch.cuda.synchronize()
+    assert torch.equal(a, f), "fused store != store + decode"
+    assert torch.equal(kp.view(torch.uint8), kp2.view(torch.uint8)) and torch.equal(sc, sc2)
+    assert_close(a, to_np64(one), torch.bfloat16, "key ranges vs unsplit")
+
+
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
 @pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256), (64, 8, 128)])
 @pytest.mark.parametrize("planned", [False, True])
