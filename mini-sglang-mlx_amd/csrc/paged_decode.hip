@@ -52,6 +52,8 @@
 //    are read exactly once per launch, so they use nontemporal (streaming)
 //    loads, which sustain markedly more HBM bandwidth for random row gathers
 //    on MI355X than default-policy loads.
+#include <atomic>
+
 #include "decode_device.h"
 
 // 0: no key-range form; split per request in chunks of one batch-wide length.
@@ -261,8 +263,8 @@ struct Resident {
   template <typename T, typename KV, int D, int G>
   int run() const {
     *ranges = decode_ranges<T, KV, D, G>();
-    static int cached[MSGL_DECODE_WAVES_PER_WG + 1] = {};
-    int& c = cached[nwaves];
+    static std::atomic<int> cached[MSGL_DECODE_WAVES_PER_WG + 1];  // per process: one device type
+    int c = cached[nwaves].load(std::memory_order_relaxed);
     if (c == 0) {
       int per_cu = 0, dev = 0, cus = 0;
       if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
@@ -274,6 +276,7 @@ struct Resident {
         return MSGL_ERR_HIP;
       }
       c = per_cu * cus > 0 ? per_cu * cus : 1;
+      cached[nwaves].store(c, std::memory_order_relaxed);
     }
     *out = c;
     return MSGL_OK;
