@@ -230,7 +230,8 @@ def test_key_ranges_long_contexts_page16(cuda_device):
     assert_close(out[pick], ref, dt, "key ranges sampled")
 
 
-def test_key_ranges_ragged_extremes(cuda_device):
+@pytest.mark.parametrize("dtype,hq", [("bf16", 16), ("f16", 32), ("bf16", 64)])
+def test_key_ranges_ragged_extremes(cuda_device, dtype, hq):
     """Key ranges over a batch with empty requests, one- and few-key requests between
     them and two requests of 400k / 350k keys (the range length is then set by the
     longest request, ceil(400000 / (S - 1))): zero rows for L = 0, the long requests
@@ -246,11 +247,11 @@ def test_key_ranges_ragged_extremes(cuda_device):
     assert n >= 2048 * 3 * cus // 2, "too few keys to select key ranges"
     indptr = np.concatenate([[0], np.cumsum(lens)]).astype(np.int32)
     indices = rng.permutation(1 << 21)[:n].astype(np.int32)
-    dt = torch.bfloat16
+    dt = DTYPES[dtype]
     kp, vp = _pools(1 << 21, 8, 128, dt, 830, cuda_device)
-    q = randn((64, 16, 128), 832, dt).to(cuda_device)
+    q = randn((64, hq, 128), 832, dt).to(cuda_device)
     ip, ix = i32(indptr, cuda_device), i32(indices, cuda_device)
-    print("case key-ranges ragged extremes", flush=True)
+    print(f"case key-ranges ragged extremes {dtype} hq={hq}", flush=True)
     out = ops.paged_decode_attention(q, kp, vp, ip, ix, 128**-0.5, max_seq_len=int(lens.max()))
     one = ops.paged_decode_attention(q, kp, vp, ip, ix, 128**-0.5, max_splits=1)
     torch.cuda.synchronize()
