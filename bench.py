@@ -1,21 +1,30 @@
 """Benchmark: the attention hot path on one MI355X.
 
-Default workload (``--workload decode``): one step = one decode step of
+Default run (``--workload headline``): the headline line plus the other
+measured workloads nested under ``workloads``, pools allocated one workload
+at a time.
+
+Headline (``--workload decode`` alone): one step = one decode step of
 Qwen3-0.6B attention over all 28 layers for a batch of 128 requests with
 ragged contexts U[200, 2048] (seed 0), page size 1, a 262144-slot bf16 KV pool
-per layer with randomly permuted slots: per layer, the new token's K/V rows
-are scattered into their slots (KV store) and paged decode attention runs over
-the pool. Inputs are resident in HBM before timing.
+per layer with randomly permuted slots: per step one decode work-list plan;
+per layer the new token's K/V rows are scattered into their slots inside the
+paged-decode launch (KV store fused), then the split-K merge launch. Inputs
+are resident in HBM before timing.
 
 Prints one JSON line. ``value`` is algorithmic GB/s over the whole step
 (decode bytes = ΣL·Hkv·D·2·2 + B·Hq·D·2·2 + ΣL·4 + (B+1)·4 per layer, plus the
-KV store's read+write); ``roofline`` is one layer's attention op alone -- the
-paged-decode kernel with the KV store fused in, plus its split-K merge kernel
--- timed with HIP events around one layer per step (rotating through the
-layers) inside the timed region, on the launch stream;
-``cpu_baseline`` times the CPU restatement of the reference's naive backend.
+KV store's read+write); ``roofline`` is the dominant kernel alone -- the
+paged-decode kernel with the KV store fused in -- timed in one layer per step
+(rotating through the layers) inside the timed region by HIP events recorded
+at that kernel's own dispatch start and end (msgl_profile_next_launch); the
+merge kernel is timed the same way and the two kernels' fraction reported
+beside it (``merge_kernel_us``, ``decode_plus_merge_frac``); ``us_per_layer``
+is the whole step over 28. ``cpu_baseline`` times the CPU
+restatement of the reference's naive backend on every host core the process
+may use.
 
-Other workloads (one JSON line each, same fields):
+Nested workloads (also runnable alone, one JSON line each):
   decode8b  paged decode, Qwen3-8B heads (32 q / 8 kv / 128), batch 256,
             context U[1024, 8192], page 16, 4M-slot pool (one layer)
   prefill   ragged chunked prefill, Qwen3-0.6B heads, 16 requests, prefix
@@ -24,11 +33,13 @@ Other workloads (one JSON line each, same fields):
   mixed     one continuous-batching step, Qwen3-8B heads, page 16, 8M-slot pool:
             128 decode requests (context U[512, 32768]) + chunks of 1024 over
             prefixes 0 and 8192, indices built on the GPU from the page table
-  decode_fp8  the default decode workload over fp8 e4m3 pools with one scale
+Other workloads (alone only):
+  decode_fp8  the headline decode over fp8 e4m3 pools with one scale
             per slot and kv head (quantising store + fp8 decode per layer)
   prefill_fp8 the prefill workload over fp8 e4m3 pools
   rope      rotate-half RoPE of q and k fused with the KV store over the
             prefill workload's 2040 packed tokens (Qwen3-0.6B heads), 28 layers
+  ceilings  a 1 GiB device copy and an 8192^3 bf16 GEMM
 """
 
 import argparse
@@ -55,8 +66,9 @@ TRAFFIC_FILE = ROOT / "profiles" / "paged_decode_b128_ctx2k_traffic.txt"
 def parse_args():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--workload", default="decode", choices=["decode", "decode8b", "decode_fp8", "prefill", "prefill_fp8", "mixed", "rope",
-                                                    "ceilings"])
+    ap.add_argument("--workload", default="headline",
+                    choices=["headline", "decode", "decode8b", "decode_fp8", "prefill", "prefill_fp8", "mixed", "rope",
+                             "ceilings"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
@@ -79,17 +91,32 @@ def read_traffic(path):
     return None
 
 
+def host_cores():
+    """Cores this process may use: its CPU affinity, capped by the cgroup's CPU
+    quota when one is set (the share the scheduler grants, whatever the
+    affinity mask lists). Returns (cores, affinity, quota or None)."""
+    aff = len(os.sched_getaffinity(0))
+    quota = None
+    try:
+        q, period = Path("/sys/fs/cgroup/cpu.max").read_text().split()[:2]
+        if q != "max":
+            quota = max(1, int(q) // int(period))
+    except (OSError, ValueError):
+        pass
+    return (min(aff, quota) if quota else aff), aff, quota
+
+
 def cpu_baseline(seconds: float):
     """The oracle's naive decode (attention/naive.py:36-60 restated in numpy, fp32)
     on the CPU reference config (B=8, L ~ U[100,1024], pool 16384, fp32) and on
-    a 16-request sample of the benchmark batch; best of repeated runs."""
+    a 16-request sample of the benchmark batch; best of repeated runs, on every
+    core the process may use."""
     import threadpoolctl
 
     import oracle
     from minisgl_hip import workloads
 
-    cores = len(os.sched_getaffinity(0))
-    cores = min(cores, 16)
+    cores, _, _ = host_cores()
     results = {}
     with threadpoolctl.threadpool_limits(cores):
         info = threadpoolctl.threadpool_info()
@@ -145,13 +172,48 @@ def main():
             torch.mul(src, 1.0, out=dst)
         torch.cuda.synchronize()
         del src, dst
-    if args.workload != "decode":
+    if args.workload not in ("decode", "headline"):
         line = {"decode8b": bench_decode8b, "prefill": bench_prefill, "mixed": bench_mixed,
                 "rope": bench_rope, "decode_fp8": bench_decode_fp8, "ceilings": bench_ceilings,
                 "prefill_fp8": lambda a, d: bench_prefill(a, d, fp8=True)}[args.workload](args, dev)
         print(json.dumps(line), flush=True)
         return
-    bench_decode(args, dev)
+    line = bench_decode(args, dev)
+    if args.workload == "headline":
+        line["workloads"] = nested_workloads(args, dev)
+    print(json.dumps(line), flush=True)
+
+
+def _traffic_ratio(name: str, algorithmic: float):
+    t = read_traffic(ROOT / "profiles" / name)
+    return None if t is None else round(t / algorithmic, 4)
+
+
+def nested_workloads(args, dev):
+    """The other measured configurations of the attention path, each on its own
+    pools (freed before the next): Qwen3-8B-head decode at batch 256 and page 16,
+    the 16-request ragged prefill, and the mixed continuous-batching step."""
+    import torch
+
+    out = {}
+    for name, fn, profile in (
+        ("decode_8b_b256_ctx8k_page16", bench_decode8b, "paged_decode_8b_b256_ctx8k_page16_traffic.txt"),
+        ("prefill_ragged_16req", bench_prefill, "prefill_ragged_16req_traffic.txt"),
+        ("mixed_step_8b_page16", bench_mixed, "mixed_step_8b_page16_traffic.txt"),
+    ):
+        torch.cuda.empty_cache()
+        print(f"# workload {name}", file=sys.stderr, flush=True)
+        line = fn(args, dev)
+        cfg = line["config"]
+        entry = {"workload": cfg["workload"], "metric": line["metric"], "value": line["value"],
+                 "unit": line["unit"], "ms_per_step": line["ms_per_step"], "roofline": line["roofline"]}
+        entry.update({k: v for k, v in cfg.items() if k != "workload"})
+        alg = cfg.get("bytes_per_step") or cfg.get("kernel_bytes")
+        entry["traffic_ratio"] = _traffic_ratio(profile, alg) if alg else None
+        out[name] = entry
+        torch.cuda.synchronize()
+    torch.cuda.empty_cache()
+    return out
 
 
 def bench_decode(args, dev):
@@ -182,25 +244,28 @@ def bench_decode(args, dev):
     def step(timed_layer=-1, events=None):
         # the step's decode work list is planned once (msgl_paged_decode_plan),
         # then per layer: the KV store of the new token fused into the
-        # paged-decode launch (msgl_paged_decode_store_planned), then the split-K
-        # merge. One layer per step is bracketed by HIP events (an event record
+        # paged-decode launch (msgl_paged_decode_planned_ex without its merge),
+        # then the split-K merge launch (msgl_paged_decode_merge) -- the same
+        # two kernels msgl_paged_decode_store_planned launches. One layer per
+        # step is bracketed by HIP events around each launch (an event record
         # costs a queue barrier, so recording around every layer would slow the
         # step down).
         ops.paged_decode_plan(indptr, None, BATCH, HQ, HKV, D, splits, ws)
         for layer in range(LAYERS):
-            if layer == timed_layer:
-                events[0].record()
+            if layer == timed_layer:  # the decode kernel's own dispatch start and end
+                ops.profile_next_launch(events[0], events[1])
             ops.paged_decode_attention(qs[layer], kps[layer], vps[layer], indptr, indices, scale,
                                        max_splits=splits, out=outs[layer], workspace=ws,
-                                       new_kv=(ks[layer], vs[layer], out_loc), planned=True)
-            if layer == timed_layer:
-                events[1].record()
+                                       new_kv=(ks[layer], vs[layer], out_loc), planned=True, merge=False)
+            if layer == timed_layer:  # the merge kernel's
+                ops.profile_next_launch(events[2], events[3])
+            ops.paged_decode_merge(outs[layer], indptr, None, HKV, splits, ws)
 
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
 
-    ev = [[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in range(args.steps)]
+    ev = _event_sets(args.steps, 4)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for s in range(args.steps):
@@ -208,16 +273,22 @@ def bench_decode(args, dev):
     torch.cuda.synchronize()
     elapsed = time.perf_counter() - t0
 
-    dec_ms = [e0.elapsed_time(e1) for (e0, e1) in ev]
-    dec_avg_s = float(np.mean(dec_ms)) / 1e3
+    # each kernel's own dispatch start to end (the span between them would also
+    # hold the delay the timing events add in front of the next dispatch)
+    kern_s = float(np.mean([e[0].elapsed_time(e[1]) for e in ev])) / 1e3  # decode kernel (store fused)
+    merge_s = float(np.mean([e[2].elapsed_time(e[3]) for e in ev])) / 1e3  # split-K merge kernel
     ms_per_step = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9
-    achieved = (dec_bytes + store_bytes) / dec_avg_s / 1e9  # one layer's decode+store launch + merge
+    achieved = (dec_bytes + store_bytes) / kern_s / 1e9  # the decode kernel alone
+    pair_achieved = (dec_bytes + store_bytes) / (kern_s + merge_s) / 1e9  # decode + merge kernels
     traffic = read_traffic(TRAFFIC_FILE)
+    del kps, vps
+    torch.cuda.empty_cache()
 
     cpu = None
     if not args.no_cpu:
         res, threads = cpu_baseline(args.cpu_seconds)
+        cores, aff, quota = host_cores()
         cpu = {
             "value": round(res["batch8_ctx1k"]["gbs"], 3),
             "unit": "GB/s",
@@ -229,13 +300,17 @@ def bench_decode(args, dev):
                 f"(B=8, L~U[100,1024] seed 0, ΣL={res['batch8_ctx1k']['sum_len']}, pool 16384, 16q/8kv/128); "
                 f"{res['batch8_ctx1k']['us_per_layer']:.0f} µs/layer. Same code on the first 16 requests of the "
                 f"benchmark batch (bf16 values as fp32, ΣL={res['batch128_sample16']['sum_len']}): "
-                f"{res['batch128_sample16']['us_per_layer']:.0f} µs/layer = {res['batch128_sample16']['gbs']:.2f} GB/s"
+                f"{res['batch128_sample16']['us_per_layer']:.0f} µs/layer = {res['batch128_sample16']['gbs']:.2f} GB/s. "
+                f"Threads: {threads} = every core the process may use (affinity {aff}, cgroup quota "
+                f"{quota if quota else 'none'})"
             ),
             "us_per_layer": round(res["batch8_ctx1k"]["us_per_layer"], 1),
             "batch128_sample16_gbs": round(res["batch128_sample16"]["gbs"], 3),
+            "host_affinity_cores": aff,
+            "host_quota_cores": quota,
         }
 
-    line = {
+    return {
         "metric": METRIC,
         "value": round(value, 2),
         "unit": "GB/s",
@@ -259,10 +334,13 @@ def bench_decode(args, dev):
             "sum_context": int(c.lens.sum()),
             "layers": LAYERS,
             "max_splits": splits,
+            "kernel_bytes": dec_bytes + store_bytes,
         },
         "us_per_layer": round(ms_per_step * 1e3 / LAYERS, 2),
         "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-        "decode_us_per_layer": round(dec_avg_s * 1e6, 2),
+        "decode_kernel_us": round(kern_s * 1e6, 2),
+        "merge_kernel_us": round(merge_s * 1e6, 2),
+        "decode_plus_merge_frac": round(pair_achieved / HBM_PEAK_GBS, 4),
         "roofline": {
             "bound": "hbm",
             "achieved": round(achieved, 2),
@@ -273,7 +351,6 @@ def bench_decode(args, dev):
         },
         "cpu_baseline": cpu,
     }
-    print(json.dumps(line), flush=True)
 
 
 def bench_decode_fp8(args, dev):
@@ -313,20 +390,23 @@ def bench_decode_fp8(args, dev):
 
     def run(i, ev):
         # per step: one plan; per layer: the fp8 decode launch that quantises and
-        # stores the new token itself (msgl_paged_decode_store_fp8_planned), then the merge
+        # stores the new token itself (without its merge), then the merge launch;
+        # one layer's decode kernel and merge kernel timed by their dispatches
         ops.paged_decode_plan(indptr, None, BATCH, HQ, HKV, D, splits, ws)
         timed = i % LAYERS
         for layer in range(LAYERS):
             kp, vp, sc = pools[layer]
             if ev and layer == timed:
-                ev[0].record()
+                ops.profile_next_launch(ev[0], ev[1])
             ops.paged_decode_attention(qs[layer], kp, vp, indptr, indices, D**-0.5, max_splits=splits,
                                        out=outs[layer], workspace=ws, planned=True, kv_scale=sc,
-                                       new_kv=(ks[layer], vs[layer], out_loc))
+                                       new_kv=(ks[layer], vs[layer], out_loc), merge=False)
             if ev and layer == timed:
-                ev[1].record()
+                ops.profile_next_launch(ev[2], ev[3])
+            ops.paged_decode_merge(outs[layer], indptr, None, HKV, splits, ws)
 
-    sec, ev_s = _timed(args, run)
+    sec, kern_s, merge_s = _timed(args, run, nev=4)
+    ev_s = kern_s
     step_bytes = LAYERS * (dec_bytes + store_bytes)
     achieved = (dec_bytes + store_bytes) / ev_s / 1e9
     line = _line(
@@ -338,7 +418,7 @@ def bench_decode_fp8(args, dev):
         "token fused into the fp8 paged decode launch + split-K merge",
         {"batch": BATCH, "sum_context": sum_l, "layers": LAYERS, "max_splits": splits,
          "bytes_per_layer": dec_bytes + store_bytes, "us_per_layer": round(sec * 1e6 / LAYERS, 2),
-         "store_decode_merge_us": round(ev_s * 1e6, 2)},
+         "decode_kernel_us": round(kern_s * 1e6, 2), "merge_kernel_us": round(merge_s * 1e6, 2)},
         {"bound": "hbm", "achieved": round(achieved, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(achieved / HBM_PEAK_GBS, 4),
          "traffic": read_traffic(ROOT / "profiles" / "paged_decode_fp8_b128_ctx2k_traffic.txt")},
@@ -347,48 +427,70 @@ def bench_decode_fp8(args, dev):
     return line
 
 
-def _timed(args, run, timed_call=None):
-    """Warm up, then time ``args.steps`` calls of run(i); ``timed_call`` (if given) is
-    bracketed by HIP events on the launch stream inside each step. Returns
-    (seconds per step, event seconds per step or None)."""
+def _event_sets(n, k):
+    """n sets of k timing events, created (recorded once) before the timed region."""
+    import torch
+
+    sets = [[torch.cuda.Event(enable_timing=True) for _ in range(k)] for _ in range(n)]
+    for es in sets:
+        for e in es:
+            e.record()
+    return sets
+
+
+def _timed(args, run, nev=2):
+    """Warm up, then time ``args.steps`` calls of run(i, events), each given a set
+    of ``nev`` timing events (created beforehand). Returns (seconds per step,
+    mean seconds between events 0 and 1, mean seconds between events 2 and 3 or
+    None)."""
     import torch
 
     for i in range(args.warmup):
         run(i, None)
     torch.cuda.synchronize()
-    ev = [[torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)] for _ in range(args.steps)]
+    ev = _event_sets(args.steps, nev)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
         run(i, ev[i])
     torch.cuda.synchronize()
     elapsed = (time.perf_counter() - t0) / args.steps
-    ev_s = float(np.mean([a.elapsed_time(b) for a, b in ev])) / 1e3
-    return elapsed, ev_s
+    ev_s = float(np.mean([e[0].elapsed_time(e[1]) for e in ev])) / 1e3
+    ev_k = float(np.mean([e[2].elapsed_time(e[3]) for e in ev])) / 1e3 if nev >= 4 else None
+    return elapsed, ev_s, ev_k
 
 
-def _b2b_step_time(args, fn, n):
+def _b2b_step_time(args, fn, n, kernel_events=False):
     """Median GPU time of one step = n calls fn(0..n-1) back to back. A spin
     kernel holds the stream while the host enqueues the step, so the events
     bracket GPU work only (the Python wrappers can need longer per call than a
-    short launch runs)."""
+    short launch runs). With ``kernel_events`` the main kernel of call s % n of
+    step s is also timed by its own dispatch timestamps; returns (median step
+    seconds, mean kernel seconds or None)."""
     import torch
+
+    from minisgl_hip import ops
 
     for _ in range(args.warmup):
         for i in range(n):
             fn(i)
     torch.cuda.synchronize()
-    times = []
-    for _ in range(args.steps):
+    times, kern = [], []
+    kev = _event_sets(args.steps, 2) if kernel_events else None
+    for s in range(args.steps):
         a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         torch.cuda._sleep(250_000 * n)  # ~120 us of spin per call: longer than the host needs to enqueue it
         a.record()
         for i in range(n):
+            if kev is not None and i == s % n:
+                ops.profile_next_launch(kev[s][0], kev[s][1])
             fn(i)
         b.record()
         torch.cuda.synchronize()
         times.append(a.elapsed_time(b) / 1e3)
-    return float(np.median(times))
+        if kev is not None:
+            kern.append(kev[s][0].elapsed_time(kev[s][1]) / 1e3)
+    return float(np.median(times)), (float(np.mean(kern)) if kern else None)
 
 
 def _line(args, metric, value, unit, ms_per_step, workload, extra, roofline, higher=True):
@@ -433,22 +535,25 @@ def bench_decode8b(args, dev):
     ws = ops.decode_workspace(batch, hq, hkv, d, splits, dev)
 
     def run(i, ev):
+        # one call: plan + decode + merge; the decode kernel timed by its dispatch
         if ev:
-            ev[0].record()
+            ev[2].record()
+            ops.profile_next_launch(ev[0], ev[1])
         ops.paged_decode_attention(q, kp, vp, pi, pid, d**-0.5, seq_lens=sl, page_size=ps, max_splits=splits,
                                    out=out, workspace=ws)
         if ev:
-            ev[1].record()
+            ev[3].record()
 
-    sec, ev_s = _timed(args, run)
+    sec, kern_s, call_s = _timed(args, run, nev=4)
     gbs = nbytes / sec / 1e9
-    ach = nbytes / ev_s / 1e9
+    ach = nbytes / kern_s / 1e9
     return _line(
         args, "paged-decode HBM GB/s, batch 256, Qwen3-8B heads, page 16", gbs, "GB/s", sec * 1e3,
         "paged decode, Qwen3-8B attention (32 q / 8 kv heads, head_dim 128), one layer; batch 256, context "
         "U[1024,8192] (seed 0), page_size 16, 4M-slot bf16 pool, random pages; split-K + merge",
         {"batch": batch, "sum_context": int(c.lens.sum()), "max_splits": splits, "bytes_per_step": nbytes,
-         "us_per_layer": round(sec * 1e6, 2)},
+         "us_per_layer": round(sec * 1e6, 2), "decode_kernel_us": round(kern_s * 1e6, 2),
+         "call_us": round(call_s * 1e6, 2)},
         {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(ach / HBM_PEAK_GBS, 4),
          "traffic": read_traffic(ROOT / "profiles" / "paged_decode_8b_b256_ctx8k_page16_traffic.txt")},
@@ -506,10 +611,11 @@ def bench_prefill(args, dev, fp8=False):
                                      max_seq_len=maxs, max_splits=splits, out=out, workspace=ws, planned=True,
                                      kv_scale=scs[layer])
 
-    step = _b2b_step_time(args, run_layer, LAYERS)
+    step, kern_s = _b2b_step_time(args, run_layer, LAYERS, kernel_events=True)
     sec = step / LAYERS  # one layer: attention + split-K merge (+ 1/28 of the plan)
     tflops = flops / sec / 1e12
     gbs = nbytes / sec / 1e9
+    k_gbs = nbytes / kern_s / 1e9  # the attention kernel alone
     line = _line(
         args, "ragged-prefill attention µs/layer, 16 requests over cached prefixes, Qwen3-0.6B heads"
         + (", fp8 KV cache" if fp8 else ""),
@@ -521,9 +627,13 @@ def bench_prefill(args, dev, fp8=False):
         "attention + split-K merge; bottom-right causal",
         {"requests": 16, "packed_tokens": t, "sum_prefix": int(case.prefix_lens.sum()), "max_splits": splits,
          "flops_per_step": flops, "bytes_per_step": nbytes, "tflops": round(tflops, 2),
-         "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4)},
-        {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-         "frac": round(gbs / HBM_PEAK_GBS, 4),
+         "mfma_frac": round(tflops / MFMA_PEAK_TFLOPS, 4), "us_per_layer": round(sec * 1e6, 2),
+         "attention_kernel_us": round(kern_s * 1e6, 2),
+         "kernel_tflops": round(flops / kern_s / 1e12, 2),
+         "kernel_mfma_frac": round(flops / kern_s / 1e12 / MFMA_PEAK_TFLOPS, 4),
+         "op_hbm_frac": round(gbs / HBM_PEAK_GBS, 4)},
+        {"bound": "hbm", "achieved": round(k_gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(k_gbs / HBM_PEAK_GBS, 4),
          "traffic": read_traffic(ROOT / "profiles" / ("prefill_ragged_16req_fp8_traffic.txt" if fp8
                                                       else "prefill_ragged_16req_traffic.txt"))},
         higher=False,
@@ -568,8 +678,8 @@ def bench_rope(args, dev):
         ops.rope(ks[layer], posd, inv, D, out=k_rot)
         ops.store_kv(k_rot, vs[layer], locd, kps[layer], vps[layer])
 
-    sec = _b2b_step_time(args, fused, LAYERS)
-    sec_unfused = _b2b_step_time(args, unfused, LAYERS)
+    sec, _ = _b2b_step_time(args, fused, LAYERS)
+    sec_unfused, _ = _b2b_step_time(args, unfused, LAYERS)
     per_launch = sec / LAYERS
     gbs = nbytes / per_launch / 1e9
     return _line(
@@ -592,7 +702,7 @@ def bench_mixed(args, dev):
     """One mixed step (GPU index build + stores + decode + prefill), Qwen3-8B heads, page 16."""
     import torch
 
-    from minisgl_hip import workloads
+    from minisgl_hip import ops, workloads
     from minisgl_hip.mixed import MixedStep
 
     hq, hkv, d, pool, ps = 32, 8, 128, 8 << 20, 16
@@ -617,21 +727,27 @@ def bench_mixed(args, dev):
     def i32(x):
         return torch.from_numpy(np.ascontiguousarray(x, dtype=np.int32)).to(dev)
 
-    step = MixedStep(i32(case.req_to_token), i32(case.table_idx), i32(case.cached_len), i32(case.device_len),
-                     num_decode=nd, num_tokens=t, num_pages=case.num_pages, max_chunk=case.max_chunk,
-                     max_seq_len=int(case.device_len.max()), num_qo_heads=hq, num_kv_heads=hkv, head_dim=d,
+    step = MixedStep(i32(case.req_to_token), case.table_idx, case.cached_len, case.device_len,
+                     num_decode=nd, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d,
                      page_size=ps, decode_splits=args.splits or None)
 
     def run(i, ev):
         if ev:
             ev[0].record()
+            if args.mixed_mode == "single":  # the mixed kernel timed by its dispatch
+                ops.profile_next_launch(ev[2], ev[3])
         step.run(q, kn, vn, kp, vp, out, d**-0.5, concurrent=args.mixed_mode == "streams",
                  single_launch=args.mixed_mode == "single")
         if ev:
             ev[1].record()
+            if args.mixed_mode != "single":
+                ev[2].record()
+                ev[3].record()
 
-    sec, ev_s = _timed(args, run)
-    ach = nbytes / ev_s / 1e9
+    sec, ev_s, kern_s = _timed(args, run, nev=4)
+    if args.mixed_mode != "single":
+        kern_s = ev_s
+    ach = nbytes / kern_s / 1e9
     return _line(
         args, "mixed continuous-batching step µs (decode + prefill + GPU index build), Qwen3-8B heads, page 16",
         sec * 1e6, "us", sec * 1e3,
@@ -643,7 +759,8 @@ def bench_mixed(args, dev):
         {"decode_requests": nd, "decode_sum_context": int(dec_lens.sum()), "prefill_tokens": int(ext.sum()),
          "decode_bytes": dec_bytes, "prefill_flops": pf_flops, "prefill_bytes": pf_bytes,
          "store_bytes": store_bytes, "decode_splits": step.decode_splits, "prefill_splits": step.prefill_splits,
-         "mode": args.mixed_mode,
+         "mode": args.mixed_mode, "bytes_per_step": nbytes, "step_events_us": round(ev_s * 1e6, 2),
+         "mixed_kernel_us": round(kern_s * 1e6, 2),
          "step_gbs": round(nbytes / sec / 1e9, 2)},
         {"bound": "hbm", "achieved": round(ach, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(ach / HBM_PEAK_GBS, 4),
@@ -668,7 +785,7 @@ def bench_ceilings(args, dev):
         if ev:
             ev[1].record()
 
-    sec, ev_s = _timed(args, copy)
+    sec, ev_s, _ = _timed(args, copy)
     copy_gbs = 2 * n / ev_s / 1e9
     del src, dst
     m = 8192
@@ -683,7 +800,7 @@ def bench_ceilings(args, dev):
         if ev:
             ev[1].record()
 
-    _, gemm_s = _timed(args, gemm)
+    _, gemm_s, _ = _timed(args, gemm)
     tflops = 2 * m**3 / gemm_s / 1e12
     return _line(
         args, "device ceilings: copy GB/s and bf16 GEMM TFLOP/s", copy_gbs, "GB/s", sec * 1e3,

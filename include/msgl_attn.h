@@ -14,7 +14,8 @@
  *   msgl_paged_decode        attention/metal.py:112-131   paged_decode_attention
  *                            (semantics of attention/naive.py:50-60 forward_decode)
  *   msgl_paged_decode_store  kvcache/pool.py:47-50 + attention/metal.py:112-131 in one launch
- *                            (+ _plan / _planned / _store_planned: plan once per step)
+ *                            (+ _plan / _planned / _store_planned: plan once per step;
+ *                            _planned_ex + _merge: the decode and split-K merge launches apart)
  *   msgl_prefill_ragged      attention/base.py:85-105     BaseAttnBackend._forward_prefill
  *                            (+ _default_splits, _workspace_size; _plan / _planned: plan once per step)
  *   msgl_build_step_indices  scheduler/scheduler.py:154-157 + attention/metal.py:145-152
@@ -29,6 +30,7 @@
  *   msgl_mixed_attention     a batch's decode requests (attention/metal.py:112-131 + the store of
  *                            kvcache/pool.py:47-50) and prefill chunks (attention/base.py:85-105)
  *                            in one launch
+ *   msgl_validate_metadata   attention/metal.py:122's precondition checks, for device-built indices
  *
  * Layouts (identical to the reference, no transposes at the boundary):
  *   q, out   [T, Hq, D]   row-major, dtype `dtype`
@@ -46,7 +48,7 @@
 extern "C" {
 #endif
 
-#define MSGL_ABI_VERSION 1
+#define MSGL_ABI_VERSION 2
 
 enum msgl_status {
   MSGL_OK = 0,
@@ -57,6 +59,17 @@ enum msgl_status {
 };
 
 enum msgl_dtype { MSGL_F32 = 0, MSGL_BF16 = 1, MSGL_F16 = 2 };
+
+/* Violations msgl_validate_metadata reports (status[0]). */
+enum msgl_meta_error {
+  MSGL_META_OK = 0,
+  MSGL_META_KV_INDPTR = 1, /* kv_indptr[0] < 0 or kv_indptr decreasing              */
+  MSGL_META_KV_RANGE = 2,  /* kv_indptr[R] beyond the entries kv_indices holds       */
+  MSGL_META_SEQ_LEN = 3,   /* a length < 0, or needing more entries than its row has */
+  MSGL_META_SLOT = 4,      /* an entry read names a slot (page) outside the pool     */
+  MSGL_META_Q_INDPTR = 5,  /* q_indptr not 0 .. num_tokens, or decreasing            */
+  MSGL_META_EXTEND = 6     /* an extend length E_r > L_r                             */
+};
 
 /* ABI version of the loaded library (MSGL_ABI_VERSION). */
 int msgl_abi_version(void);
@@ -95,8 +108,9 @@ int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, in
  * equals attention/naive.py:50-60 (gather + masked SDPA) within fp tolerance.
  *
  *   q          [B, Hq, D]
- *   kv_indptr  CSR offsets into kv_indices ([B+1]); when seq_lens != NULL only
- *              kv_indptr[0..B-1] are read (start offsets, any order)
+ *   kv_indptr  CSR offsets into kv_indices ([B+1]); kv_indptr[B] is the number
+ *              of entries kv_indices holds (reads stop there); with seq_lens the
+ *              rows' start offsets may come in any order
  *   kv_indices page_size == 1: token slots (attention/metal.py:150);
  *              page_size  > 1: page ids; token t of a request lives at slot
  *              kv_indices[kv_indptr[b] + t / page_size] * page_size + t % page_size
@@ -111,8 +125,10 @@ int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, in
  *   workspace  >= msgl_paged_decode_workspace_size(B, Hq, Hkv, D, max_splits)
  *              bytes, 256-byte aligned
  * Launches the decode kernel and, when max_splits > 1, the split-K merge.
- * A request with L_b == 0 gets a zero output row. Slots outside
- * [0, num_slots) are clamped to slot 0 (memory-safe; result unspecified).
+ * A request with L_b == 0 gets a zero output row. Memory-safe for any
+ * metadata: index entries past kv_indptr[B] are not read and slots outside
+ * [0, num_slots) read slot 0 (the result is then unspecified;
+ * msgl_validate_metadata reports such metadata as an error).
  */
 int msgl_paged_decode(const void* q, const void* k_pool, const void* v_pool, const int32_t* kv_indptr,
                       const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
@@ -163,7 +179,9 @@ int64_t msgl_prefill_workspace_size(int32_t num_reqs, int32_t num_tokens, int32_
  * arguments as msgl_paged_decode / msgl_paged_decode_store and use that plan
  * instead of building it (one launch fewer per call). The plan must have been
  * built on the same stream, for the same index data, workspace and sizes, and
- * the workspace must not be re-planned before the calls that use it. No
+ * the workspace must not be re-planned before the calls that use it. The plan
+ * records the batch, max_splits and kv-head count it was built for; a planned
+ * launch whose sizes differ does nothing (no work item is read). No
  * reference counterpart (MLX decodes layer by layer, attention/metal.py:112-131).
  */
 int msgl_paged_decode_plan(const int32_t* kv_indptr, const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
@@ -182,6 +200,37 @@ int msgl_paged_decode_store_planned(const void* q, const void* k_new, const void
                                     int64_t workspace_bytes, void* stream);
 
 /*
+ * The planned decode family in one entry point, with launch flags:
+ * k_new/v_new/out_loc all NULL (msgl_paged_decode_planned) or all set
+ * (msgl_paged_decode_store_planned), kv_scale NULL (unquantised pools) or the
+ * fp8 pools' scales (the _fp8_ forms). MSGL_DECODE_NO_MERGE launches the
+ * decode kernel only: requests in one chunk get their output rows, the others
+ * leave split-K partials in the workspace for msgl_paged_decode_merge (the two
+ * calls on one stream equal the call without the flag, bit for bit). No
+ * reference counterpart; it lets a caller time or schedule the two launches
+ * apart.
+ */
+#define MSGL_DECODE_NO_MERGE 1u
+int msgl_paged_decode_planned_ex(const void* q, const void* k_new, const void* v_new, const int32_t* out_loc,
+                                 void* k_pool, void* v_pool, float* kv_scale, const int32_t* kv_indptr,
+                                 const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
+                                 int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                 int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, uint32_t flags,
+                                 void* out, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * The split-K merge of a planned decode launched with MSGL_DECODE_NO_MERGE:
+ * out[b] = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s over the chunks of
+ * every request cut into more than one (the combine of the Metal kernel's
+ * simdgroup merge, attention/metal.py:75-94). Same indices, sizes, dtype,
+ * max_splits and workspace as the decode call; nothing to do when
+ * max_splits == 1.
+ */
+int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                            int32_t num_kv_heads, int32_t head_dim, int32_t dtype, int32_t max_splits, void* out,
+                            void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
  * Ragged chunked-prefill attention over a paged pool, one launch per batch.
  * Replaces attention/base.py:85-105 (BaseAttnBackend._forward_prefill, a
  * per-request MLX SDPA loop).
@@ -189,7 +238,8 @@ int msgl_paged_decode_store_planned(const void* q, const void* k_new, const void
  *   q          [T, Hq, D] packed extend tokens; request i owns rows
  *              q_indptr[i] .. q_indptr[i+1]-1 (E_i rows); T = num_tokens =
  *              q_indptr[R]
- *   kv_indptr  offsets into kv_indices ([R+1]; with seq_lens only [R] read)
+ *   kv_indptr  offsets into kv_indices ([R+1]; kv_indptr[R] = entries of
+ *              kv_indices, where reads stop)
  *   kv_indices slots (page ids when page_size > 1) of request i's full KV:
  *              the cached prefix followed by this step's E_i rows, which the
  *              caller stored with msgl_store_kv first
@@ -207,7 +257,9 @@ int msgl_paged_decode_store_planned(const void* q, const void* k_new, const void
  *              (fp32: may be NULL). Consecutive calls on one stream may share it.
  *   out        [T, Hq, D]
  * Query t of request i sees keys j <= P_i + t (MLX's bottom-right causal
- * mask, docs/04-attention.md:35-36); E_i <= L_i is required.
+ * mask, docs/04-attention.md:35-36); E_i <= L_i is required. Memory-safe for
+ * any metadata (q rows outside [0, num_tokens) are neither read nor written,
+ * index reads stop at kv_indptr[R]); msgl_validate_metadata checks it.
  */
 int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, const int32_t* q_indptr,
                         const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
@@ -223,7 +275,8 @@ int msgl_prefill_ragged(const void* q, const void* k_pool, const void* v_pool, c
  * msgl_prefill_ragged_planned (the arguments of msgl_prefill_ragged) runs the
  * attention from it, skipping one launch per layer. Same workspace, sizes,
  * dtype and max_splits in both calls, on one stream; fp32 has no work list
- * (the plan is a no-op).
+ * (the plan is a no-op). The plan records the sizes it was built for; a
+ * planned launch whose sizes differ does nothing.
  */
 int msgl_prefill_plan(const int32_t* q_indptr, const int32_t* kv_indptr, const int32_t* seq_lens, int32_t num_reqs,
                       int32_t num_tokens, int32_t max_extend_len, int32_t max_seq_len, int32_t num_qo_heads,
@@ -403,6 +456,33 @@ int msgl_mixed_attention(const void* q_dec, const void* k_new, const void* v_new
                          int32_t pf_max_splits, void* out_pf, void* pf_workspace, int64_t pf_workspace_bytes,
                          void* k_pool, void* v_pool, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                          int32_t page_size, int64_t num_slots, int32_t dtype, float scale, void* stream);
+
+/*
+ * Instrumentation: the calling thread's next main-kernel launch -- the decode
+ * kernel of a decode call, the merge of msgl_paged_decode_merge, the attention
+ * kernel of a prefill call or the mixed-step kernel -- records start_event and
+ * stop_event (hipEvent_t, created by the caller) at its own dispatch start and
+ * end (hipExtLaunchKernel), so hipEventElapsedTime gives that kernel's
+ * duration without the queue barrier an event record before the call adds.
+ * One launch consumes them; NULL, NULL disarms. No reference counterpart.
+ */
+int msgl_profile_next_launch(void* start_event, void* stop_event);
+
+/*
+ * Opt-in check of the index metadata of a decode (q_indptr NULL) or prefill
+ * call, on the device, before the attention launches read it. Counterpart of
+ * the reference's host-side preconditions (attention/metal.py:122) for indices
+ * that never reach the host. Walks exactly the entries the attention kernels
+ * read (request r: kv_indices[kv_indptr[r] .. + L_r, or ceil(L_r / page_size)
+ * page ids]) and never reads past num_indices entries of kv_indices or the
+ * [R+1] offsets. status: int64[3] device words, cleared by the call, then
+ * {msgl_meta_error code, request or entry index, offending value} of one
+ * violation found (0 = none). Two launches; the caller reads status after
+ * synchronising.
+ */
+int msgl_validate_metadata(const int32_t* kv_indptr, const int32_t* kv_indices, const int32_t* seq_lens,
+                           const int32_t* q_indptr, int32_t num_reqs, int32_t page_size, int64_t num_indices,
+                           int64_t num_slots, int32_t num_tokens, int64_t* status, void* stream);
 
 #ifdef __cplusplus
 }

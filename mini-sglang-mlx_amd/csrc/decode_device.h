@@ -86,14 +86,16 @@ __device__ __forceinline__ void split_geometry(int L, int max_splits, int chunk_
   n = min(max_splits, (L + chunk - 1) / chunk);
 }
 
-__device__ __forceinline__ int slot_of(const int32_t* __restrict__ kv_indices, int start, int tok, int page_size,
-                                       int64_t num_slots) {
-  int64_t s;
-  if (page_size == 1) {
-    s = kv_indices[start + tok];
-  } else {
-    s = (int64_t)kv_indices[start + tok / page_size] * page_size + tok % page_size;
-  }
+// Pool slot of token `tok` of the request whose indices start at kv_indices[start].
+// Memory-safe for any metadata: an index entry outside [0, nidx) (nidx =
+// kv_indptr[B], the entries kv_indices holds) is not read, and a slot outside
+// [0, num_slots) is replaced by slot 0 (the result is then unspecified; the
+// metadata validation reports both).
+__device__ __forceinline__ int slot_of(const int32_t* __restrict__ kv_indices, int64_t nidx, int start, int tok,
+                                       int page_size, int64_t num_slots) {
+  const int64_t i = (int64_t)start + (page_size == 1 ? tok : tok / page_size);
+  if (i < 0 || i >= nidx) return 0;
+  const int64_t s = page_size == 1 ? (int64_t)kv_indices[i] : (int64_t)kv_indices[i] * page_size + tok % page_size;
   return (s >= 0 && s < num_slots) ? (int)s : 0;
 }
 
@@ -137,7 +139,9 @@ struct DecodeParams {
   void* v_pool_w;
   // work list (plan kernel output, in the workspace)
   int* meta;        // [0] items in the plan, [1] batch-wide chunk length, [2] the plan's max_splits
-                    // (with key offsets), [3] max_b L_b
+                    // (with key offsets), [3] max_b L_b, [4..6] the batch, max_splits and kv-head
+                    // groups the plan was built for, [7] the key ranges the last decode launch
+                    // over this plan split by (0: per-request chunks), read by the merge
   int4* plan;       // (request, split, kv-head group, 0), longest first
   int64_t* tok_off; // balanced split: [B+1] tokens of the requests before b (tok_off[B] = all)
   int nranges;      // balanced split: key ranges of the launch (grid / ngrp)
@@ -145,15 +149,24 @@ struct DecodeParams {
   int hq, hkv, page_size, max_splits, batch, ngrp;
   bool planned;   // the workspace already holds this call's plan
   bool balanced;  // equal key ranges of the batch's token stream allowed (else per-request chunks)
+  bool skip_merge;  // host side: launch the decode kernel only (msgl_paged_decode_merge follows)
   float scale_log2;
 };
+
+// The work list in the workspace was built for this call's batch, split bound
+// and kv-head groups (the plan kernel stamps them into meta[4..6]). A launch
+// over a plan of other sizes does nothing: its items would index other
+// requests and workspace regions.
+__device__ __forceinline__ bool plan_matches(const DecodeParams& p) {
+  return p.meta[4] == p.batch && p.meta[5] == p.max_splits && p.meta[6] == p.ngrp && p.meta[1] >= 16;
+}
 
 // Whether this launch splits by equal key ranges: allowed, the plan wrote key
 // offsets for this max_splits, and the batch's keys (tok_off[B]) average at
 // least MSGL_DECODE_BALANCED_MIN_RANGE per range. Used identically by the
 // decode and merge kernels; otherwise both follow the per-request work list.
 __device__ __forceinline__ bool balanced_launch(const DecodeParams& p) {
-  return p.balanced && p.meta[2] == p.max_splits &&
+  return p.balanced && plan_matches(p) && p.meta[2] == p.max_splits &&
          p.tok_off[p.batch] >= (int64_t)MSGL_DECODE_BALANCED_MIN_RANGE * p.nranges;
 }
 
@@ -228,6 +241,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
   uint8_t* K_lds = reinterpret_cast<uint8_t*>(lds + kLdsPerWave);  // [16][KRS bytes]
 
   const int64_t row_stride = (int64_t)p.hkv * D * EKV;  // bytes per slot
+  const int64_t nidx = p.kv_indptr[p.batch];             // entries of kv_indices
 
   // One chunk: keys [t0, t1) of request b (L keys, kv_indices from start),
   // partial `split` of its n; the kv-head group kgrp is this workgroup's waves.
@@ -325,7 +339,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
       __syncthreads();
       for (int i = threadIdx.x; i < (ntile + NST - 1) * 16; i += blockDim.x) {
         const int tok = s0 + min(i, seg_len - 1);
-        slots_lds[i] = slot_of(p.kv_indices, start, tok, p.page_size, p.num_slots);
+        slots_lds[i] = slot_of(p.kv_indices, nidx, start, tok, p.page_size, p.num_slots);
       }
       __syncthreads();
       if (!active) continue;
@@ -494,6 +508,9 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
   // ranges it overlaps. Otherwise: one work item of the plan (workgroups past
   // its end have nothing to do).
   const bool bal = RANGES && balanced_launch(p);
+  // the form this launch splits by, for the merge (which need not know the
+  // kernel's residency or whether key ranges were built in)
+  if (wg == 0 && threadIdx.x == 0 && plan_matches(p)) p.meta[7] = bal ? p.nranges : 0;
   int b, kgrp, start = 0, L = 0, t0 = 0, t1 = 0, split = 0, n = 1;
   int64_t k = 0, rl = 1, g0 = 0, g1 = 0;
   if (bal) {
@@ -517,7 +534,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
     }
     b = lo;
   } else {
-    if (wg >= p.meta[0]) return;
+    if (wg >= p.meta[0] || !plan_matches(p)) return;
     const int4 item = p.plan[wg];
     b = item.x;
     split = item.y;
@@ -569,15 +586,17 @@ __device__ __forceinline__ void paged_decode_merge_body(const DecodeParams& p, i
   const int lane = threadIdx.x & 63;
   if (unit >= batch * p.hkv) return;
   const int b = unit / p.hkv, kvh = unit % p.hkv;
+  if (!plan_matches(p)) return;
   int n, chunk;
-  if (balanced_launch(p)) {  // the ranges request b overlaps; no key: the defined zero output
+  const int nranges = p.meta[7];  // the key ranges the decode launch split by (0: per-request chunks)
+  if (nranges > 0) {  // the ranges request b overlaps; no key: the defined zero output
     const int64_t ob = p.tok_off[b], ob1 = p.tok_off[b + 1];
     if (ob1 == ob) {
       T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D;
       for (int i = lane; i < G * D; i += 64) o[i] = from_f32<T>(0.f);
       return;
     }
-    const int64_t rl = balanced_range(p.tok_off[p.batch], p.meta[3], p.nranges, p.max_splits);
+    const int64_t rl = balanced_range(p.tok_off[p.batch], p.meta[3], nranges, p.max_splits);
     n = (int)((ob1 - 1) / rl - ob / rl + 1);
   } else {
     const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];

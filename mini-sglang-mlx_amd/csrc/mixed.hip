@@ -74,18 +74,12 @@ int launch_mixed(pf::PrefillParams pp, const dec::DecodeParams& dp, int batch, i
   pp.items = (int)items_pf;
   const int64_t items_dec = dec::decode_items(dp);
   const size_t lds = std::max<size_t>(Geo::LDS_BYTES, dec::decode_lds_bytes<T, D>(4));
-  static bool attr_set = false;  // per process; the attribute is per function
-  if (lds > 65536 && !attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&mixed_attention_kernel<T, D, G>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess) {
-      set_error("msgl_mixed_attention: cannot raise the LDS limit to %zu bytes", lds);
-      return MSGL_ERR_HIP;
-    }
-    attr_set = true;
-  }
+  static std::atomic<uint64_t> lds_raised{0};  // per device, for this instantiation
+  const int lst = ensure_lds_limit(reinterpret_cast<const void*>(&mixed_attention_kernel<T, D, G>), (int)lds,
+                                   lds_raised, "msgl_mixed_attention");
+  if (lst != MSGL_OK) return lst;
   const int64_t groups = (items_pf + 7) / 8 + (items_dec + 7) / 8;
-  hipLaunchKernelGGL((mixed_attention_kernel<T, D, G>), dim3((unsigned)(8 * groups)), dim3(256), lds, stream, pp,
-                     dp);
+  launch_main(mixed_attention_kernel<T, D, G>, dim3((unsigned)(8 * groups)), dim3(256), lds, stream, pp, dp);
   MSGL_CHECK_LAUNCH("msgl_mixed_attention");
   constexpr int HPB = 256 / (D / 4);  // heads per prefill-merge workgroup
   const int npm = pp.splits > 1 ? pp.num_tokens * ((pp.hq + HPB - 1) / HPB) : 0;

@@ -1,9 +1,11 @@
 // Shared device helpers and host error channel for the gfx950 attention kernels.
 #pragma once
 
+#include <hip/hip_ext.h>
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
 #include <cstdio>
 #include <string>
 
@@ -16,6 +18,22 @@ namespace msgl {
 // ---------------------------------------------------------------------------
 void set_error(const char* fmt, ...);
 void clear_error();
+
+// The events msgl_profile_next_launch armed for this thread, if any (disarms them).
+bool take_profile_events(hipEvent_t& start, hipEvent_t& stop);
+
+// Launch of an entry point's main kernel: with events armed by
+// msgl_profile_next_launch, through hipExtLaunchKernel, which records them at
+// the dispatch's own start and end (no queue barrier in front of the kernel).
+template <typename K, typename... Args>
+inline void launch_main(K kernel, dim3 grid, dim3 block, size_t lds, hipStream_t stream, Args... args) {
+  hipEvent_t e0, e1;
+  if (take_profile_events(e0, e1)) {
+    hipExtLaunchKernelGGL(kernel, grid, block, (std::uint32_t)lds, stream, e0, e1, 0u, args...);
+  } else {
+    hipLaunchKernelGGL(kernel, grid, block, lds, stream, args...);
+  }
+}
 
 #define MSGL_CHECK_ARG(cond, ...)            \
   do {                                       \
@@ -33,6 +51,26 @@ void clear_error();
       return MSGL_ERR_HIP;                                                               \
     }                                                                                    \
   } while (0)
+
+// Raises `fn`'s dynamic-LDS limit to `bytes` once per device: `done` (one per
+// kernel function) holds a bit per device id that already has it. Concurrent
+// first calls may both set the attribute, which is harmless (it is idempotent).
+inline int ensure_lds_limit(const void* fn, int bytes, std::atomic<uint64_t>& done, const char* what) {
+  if (bytes <= 65536) return MSGL_OK;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) {
+    set_error("%s: hipGetDevice failed", what);
+    return MSGL_ERR_HIP;
+  }
+  const uint64_t bit = dev < 64 ? (uint64_t)1 << dev : 0;
+  if (bit != 0 && (done.load(std::memory_order_acquire) & bit)) return MSGL_OK;
+  if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) {
+    set_error("%s: cannot raise the LDS limit to %d bytes", what, bytes);
+    return MSGL_ERR_HIP;
+  }
+  done.fetch_or(bit, std::memory_order_acq_rel);
+  return MSGL_OK;
+}
 
 inline int dtype_size(int32_t dtype) {
   switch (dtype) {

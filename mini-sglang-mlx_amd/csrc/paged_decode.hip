@@ -215,6 +215,9 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeP
       run += c;
     }
     p.meta[0] = run * p.ngrp;
+    p.meta[4] = p.batch;  // the sizes this list is for (checked by every launch that reads it)
+    p.meta[5] = p.max_splits;
+    p.meta[6] = p.ngrp;
   }
   __syncthreads();
   for (int t = threadIdx.x; t < ncand; t += kPlanThreads) {
@@ -235,16 +238,30 @@ static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
     hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
     MSGL_CHECK_LAUNCH("msgl_paged_decode (plan)");
   }
-  hipLaunchKernelGGL((paged_decode_kernel<T, KV, D, G>), dim3((unsigned)dec::decode_items(p)), dim3(64 * nwaves),
-                     lds, stream, p);
+  launch_main(paged_decode_kernel<T, KV, D, G>, dim3((unsigned)dec::decode_items(p)), dim3(64 * nwaves), lds, stream,
+              p);
   MSGL_CHECK_LAUNCH("msgl_paged_decode");
-  if (p.max_splits > 1) {
+  if (p.max_splits > 1 && !p.skip_merge) {
     const int units = batch * p.hkv;
     hipLaunchKernelGGL((paged_decode_merge_kernel<T, D, G>), dim3((units + 3) / 4), dim3(256), 0, stream, p, batch);
     MSGL_CHECK_LAUNCH("msgl_paged_decode (merge)");
   }
   return MSGL_OK;
 }
+
+// The split-K merge launch on its own (msgl_paged_decode_merge).
+struct MergeLaunch {
+  const DecodeParams& p;
+  int batch;
+  hipStream_t stream;
+  template <typename T, typename KV, int D, int G>
+  int run() const {
+    const int units = batch * p.hkv;
+    launch_main(paged_decode_merge_kernel<T, D, G>, dim3((units + 3) / 4), dim3(256), 0, stream, p, batch);
+    MSGL_CHECK_LAUNCH("msgl_paged_decode_merge");
+    return MSGL_OK;
+  }
+};
 
 struct Launch {
   const DecodeParams& p;
@@ -413,7 +430,7 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
                              const int32_t* seq_lens,
                              int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                              int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
-                             void* out, void* workspace, int64_t workspace_bytes, void* stream);
+                             void* out, void* workspace, int64_t workspace_bytes, void* stream, uint32_t flags = 0);
 
 extern "C" int msgl_paged_decode(const void* q, const void* k_pool, const void* v_pool, const int32_t* kv_indptr,
                                  const int32_t* kv_indices, const int32_t* seq_lens, int32_t batch,
@@ -645,6 +662,7 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
   p.max_splits = max_splits;
   p.scale_log2 = scale * kLog2e;
   p.balanced = false;
+  p.skip_merge = false;
   p.nranges = 1;
   if (max_splits > 1) {
     const int nwaves = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
@@ -665,7 +683,7 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
                              const int32_t* seq_lens,
                              int32_t batch, int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim,
                              int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
-                             void* out, void* workspace, int64_t workspace_bytes, void* stream) {
+                             void* out, void* workspace, int64_t workspace_bytes, void* stream, uint32_t flags) {
   using namespace msgl;
   DecodeParams p;
   bool empty = false;
@@ -674,6 +692,74 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
                                     page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, p,
                                     empty);
   if (st != MSGL_OK || empty) return st;
+  p.skip_merge = (flags & MSGL_DECODE_NO_MERGE) != 0;
   return dispatch(Launch{p, batch, (hipStream_t)stream}, dtype, kv_scale != nullptr, head_dim,
                   num_qo_heads / num_kv_heads, fn);
+}
+
+extern "C" int msgl_paged_decode_planned_ex(const void* q, const void* k_new, const void* v_new,
+                                            const int32_t* out_loc, void* k_pool, void* v_pool, float* kv_scale,
+                                            const int32_t* kv_indptr, const int32_t* kv_indices,
+                                            const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                            int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                            int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                                            uint32_t flags, void* out, void* workspace, int64_t workspace_bytes,
+                                            void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG((flags & ~(uint32_t)MSGL_DECODE_NO_MERGE) == 0, "msgl_paged_decode_planned_ex: unknown flags 0x%x",
+                 flags);
+  MSGL_CHECK_ARG((k_new == nullptr) == (v_new == nullptr) && (k_new == nullptr) == (out_loc == nullptr),
+                 "msgl_paged_decode_planned_ex: k_new, v_new and out_loc go together");
+  MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
+                 "msgl_paged_decode_planned_ex: k_new and v_new must be 16-byte aligned");
+  return paged_decode_impl("msgl_paged_decode_planned_ex", kRunPlanned, q, k_new, v_new, out_loc, k_pool, v_pool,
+                           kv_scale, kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim,
+                           page_size, num_slots, dtype, scale, max_splits, out, workspace, workspace_bytes, stream,
+                           flags);
+}
+
+extern "C" int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* seq_lens, int32_t batch,
+                                       int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
+                                       int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
+                                       void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(batch >= 0 && batch <= 65535, "msgl_paged_decode_merge: batch must be in [0, 65535]");
+  if (batch == 0) return MSGL_OK;
+  MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0 && num_qo_heads % num_kv_heads == 0,
+                 "msgl_paged_decode_merge: bad head counts");
+  MSGL_CHECK_ARG(kv_indptr != nullptr && out != nullptr, "msgl_paged_decode_merge: null kv_indptr or out");
+  MSGL_CHECK_ARG((uintptr_t)out % 16 == 0, "msgl_paged_decode_merge: out must be 16-byte aligned");
+  if (dtype_size(dtype) == 0) {
+    set_error("msgl_paged_decode_merge: unknown dtype %d", dtype);
+    return MSGL_ERR_UNSUPPORTED;
+  }
+  if (max_splits <= 0) max_splits = msgl_paged_decode_default_splits(batch, num_kv_heads, 0);
+  if (max_splits > kMaxSplits) max_splits = kMaxSplits;
+  const int64_t need = msgl_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
+  if (workspace == nullptr || workspace_bytes < need || (uintptr_t)workspace % 256 != 0) {
+    set_error("msgl_paged_decode_merge: 256-byte aligned workspace of %lld bytes needed, %lld given",
+              (long long)need, (long long)workspace_bytes);
+    return MSGL_ERR_WORKSPACE;
+  }
+  if (max_splits == 1) return MSGL_OK;  // every request was written by the decode launch
+  DecodeParams p{};
+  const DecodeWorkspace w = decode_workspace(batch, num_qo_heads, num_kv_heads, head_dim, max_splits);
+  uint8_t* ws = reinterpret_cast<uint8_t*>(workspace);
+  p.kv_indptr = kv_indptr;
+  p.seq_lens = seq_lens;
+  p.out = out;
+  p.meta = reinterpret_cast<int*>(ws);
+  p.plan = reinterpret_cast<int4*>(ws + w.plan);
+  p.tok_off = reinterpret_cast<int64_t*>(ws + w.tok_off);
+  p.part_ml = reinterpret_cast<float*>(ws + w.part_ml);
+  p.part_o = reinterpret_cast<float*>(ws + w.part_o);
+  p.batch = batch;
+  p.hq = num_qo_heads;
+  p.hkv = num_kv_heads;
+  p.max_splits = max_splits;
+  p.ngrp = decode_groups(num_kv_heads);
+  return dispatch(MergeLaunch{p, batch, (hipStream_t)stream}, dtype, false, head_dim, num_qo_heads / num_kv_heads,
+                  "msgl_paged_decode_merge");
 }

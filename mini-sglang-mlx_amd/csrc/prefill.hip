@@ -112,6 +112,12 @@ __global__ __launch_bounds__(kPlanThreads) void prefill_plan_kernel(PrefillParam
       run += c;
     }
     *p.plan_count = run * p.hkv;
+    p.plan_count[1] = p.num_reqs;  // the sizes this list is for (checked by every launch that reads it)
+    p.plan_count[2] = p.num_tokens;
+    p.plan_count[3] = p.splits;
+    p.plan_count[4] = p.nqb;
+    p.plan_count[5] = p.hkv;
+    p.plan_count[6] = p.chunk_len;
   }
   __syncthreads();
   for (int t = threadIdx.x; t < ntrip; t += kPlanThreads) {
@@ -186,6 +192,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
   const int qb = blockIdx.x * BQ;
   if (qb >= E) return;
   const int kv_start = p.kv_indptr[req];
+  const int64_t nidx = p.kv_indptr[p.num_reqs];  // entries of kv_indices
   const int Lkv = p.seq_lens ? p.seq_lens[req] : (p.kv_indptr[req + 1] - kv_start);
   const int P = Lkv - E;
   const int kv_end = block_kv_end(Lkv, E, qb, BQ);
@@ -199,7 +206,8 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
   constexpr int NQF = D / 16;
   u32x4 qf[NQF];
   {
-    const uint8_t* qrow = reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + my_tok) * p.hq + my_head) * D * 4;
+    const int64_t qr = min((int64_t)max(q0 + my_tok, 0), (int64_t)p.num_tokens - 1);  // q holds num_tokens rows
+    const uint8_t* qrow = reinterpret_cast<const uint8_t*>(p.q) + (qr * p.hq + my_head) * D * 4;
 #pragma unroll
     for (int j = 0; j < NQF; ++j) qf[j] = ld16(qrow + (16 * j + 4 * grp) * 4);
   }
@@ -224,7 +232,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
 #pragma unroll
     for (int i = 0; i < CH; ++i) {
       const int j = kt0 + (tid + 256 * i) / CPR;
-      nslot[i] = j < kv_end ? (int)kv_slot(p, kv_start, j) : -1;
+      nslot[i] = j < kv_end ? (int)kv_slot(p, nidx, kv_start, j) : -1;
     }
   };
   auto gload = [&]() {
@@ -345,7 +353,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
     const int row = wave * QROWS32 + 4 * grp + i;
     const int tok = qb + row / G;
     const float rinv = __shfl(inv, 4 * grp + i);
-    if (tok < E) {
+    if (tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {
       float* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
       for (int t = 0; t < NDT; ++t) orow[t * 16 + col] = acc[t][i] * rinv;
@@ -375,16 +383,11 @@ int launch16(PrefillParams p, int max_e, hipStream_t stream) {
   }
   if (p.mode == kPlanOnly) return MSGL_OK;
   const int grid = (int)items;
-  static bool attr_set = false;  // per process; the attribute is per function
-  if (Geo::LDS_BYTES > 65536 && !attr_set) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&prefill16_kernel<T, KV, D, G>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, Geo::LDS_BYTES) != hipSuccess) {
-      set_error("msgl_prefill_ragged: cannot raise the LDS limit to %d bytes", Geo::LDS_BYTES);
-      return MSGL_ERR_HIP;
-    }
-    attr_set = true;
-  }
-  hipLaunchKernelGGL((prefill16_kernel<T, KV, D, G>), dim3(grid), dim3(THREADS16), Geo::LDS_BYTES, stream, p);
+  static std::atomic<uint64_t> lds_raised{0};  // per device, for this instantiation
+  const int lst = ensure_lds_limit(reinterpret_cast<const void*>(&prefill16_kernel<T, KV, D, G>), Geo::LDS_BYTES,
+                                   lds_raised, "msgl_prefill_ragged");
+  if (lst != MSGL_OK) return lst;
+  launch_main(prefill16_kernel<T, KV, D, G>, dim3(grid), dim3(THREADS16), Geo::LDS_BYTES, stream, p);
   MSGL_CHECK_LAUNCH("msgl_prefill_ragged");
   if (p.splits > 1) {
     constexpr int HPB = 256 / (D / 4);
@@ -399,8 +402,7 @@ template <int D, int G>
 int launch32(const PrefillParams& p, int max_e, hipStream_t stream) {
   constexpr int BQ = NWAVE * QROWS32 / G;
   const int qblocks = (max_e + BQ - 1) / BQ;
-  hipLaunchKernelGGL((prefill_f32_kernel<D, G>), dim3(qblocks, p.num_reqs * p.hkv), dim3(256), G32<D>::LDS_BYTES,
-                     stream, p);
+  launch_main(prefill_f32_kernel<D, G>, dim3(qblocks, p.num_reqs * p.hkv), dim3(256), G32<D>::LDS_BYTES, stream, p);
   MSGL_CHECK_LAUNCH("msgl_prefill_ragged");
   return MSGL_OK;
 }

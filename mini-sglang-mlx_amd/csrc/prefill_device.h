@@ -38,7 +38,7 @@ struct PrefillParams {
   float2* part_ml;   // [splits][num_tokens][hq]
   int4* plan;        // work list, longest first: per item (request, kv head, query block, chunk)
                      // then (first token, extend length E, first kv index, kv length L)
-  int* plan_count;   // its length
+  int* plan_count;   // its length, then the sizes the list was built for (plan_matches)
   int* merge_n;      // [num_tokens] chunks of each token's block (<= 1: nothing to merge)
   int64_t num_slots;
   int hq, hkv, page_size;
@@ -56,14 +56,24 @@ struct PrefillParams {
 // attention with a work list already in the workspace, or only the work list.
 enum PrefillMode { kPlanAndRun = 0, kRunPlanned = 1, kPlanOnly = 2 };
 
-__device__ __forceinline__ int64_t kv_slot(const PrefillParams& p, int start, int tok) {
-  int64_t s;
-  if (p.page_size == 1) {
-    s = p.kv_indices[start + tok];
-  } else {
-    s = (int64_t)p.kv_indices[start + tok / p.page_size] * p.page_size + tok % p.page_size;
-  }
+// Pool slot of token `tok` of the request whose indices start at
+// kv_indices[start]; memory-safe for any metadata: an index entry outside
+// [0, nidx) (nidx = kv_indptr[R], the entries kv_indices holds) is not read,
+// and a slot outside [0, num_slots) becomes slot 0.
+__device__ __forceinline__ int64_t kv_slot(const PrefillParams& p, int64_t nidx, int start, int tok) {
+  const int64_t i = (int64_t)start + (p.page_size == 1 ? tok : tok / p.page_size);
+  if (i < 0 || i >= nidx) return 0;
+  const int64_t s = p.page_size == 1 ? (int64_t)p.kv_indices[i] : (int64_t)p.kv_indices[i] * p.page_size + tok % p.page_size;
   return (s >= 0 && s < p.num_slots) ? s : 0;
+}
+
+// The work list in the workspace was built for this call's sizes: the plan
+// kernel stamps (requests, tokens, splits, query blocks, kv heads, chunk
+// length) after its length. A launch over a plan of other sizes does nothing.
+__device__ __forceinline__ bool plan_matches(const PrefillParams& p) {
+  const int* st = p.plan_count;
+  return st[1] == p.num_reqs && st[2] == p.num_tokens && st[3] == p.splits && st[4] == p.nqb && st[5] == p.hkv &&
+         st[6] == p.chunk_len;
 }
 
 // Keys a block of query tokens [qb, qb + bq) can see.
@@ -109,13 +119,37 @@ __device__ __forceinline__ uint2 lds_read_tr16<f16_t>(const uint8_t* p) {
   return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(lp));
 }
 
-// 16 bytes per lane from global memory into LDS at m0 + 16 * lane. Issued as
-// inline assembly so the compiler does not drain every outstanding transfer
-// before the next LDS read; the caller waits with vm_wait.
+// LDS DMA (global_load_lds_dword{,x4}): `bytes` per lane from global memory
+// into LDS at lds_addr + bytes * lane (lds_addr wave-uniform, in m0). The
+// caller waits for the transfer with vm_wait and makes it visible to the
+// other wavefronts with a barrier.
+//
+// Issued as inline assembly: with __builtin_amdgcn_global_load_lds the
+// compiler cannot tell which LDS bytes a transfer in flight writes (it has no
+// alias scopes for them), so it drains every transfer (vmcnt(0)) before each
+// LDS read of the ring, which serialises the pipeline below. The statement is
+// self-contained: it saves m0, sets it, waits the one wait state an SALU write
+// of m0 needs before an LDS DMA reads it (GFX9 family), issues the transfer
+// and restores m0, so whatever the compiler keeps in m0 survives it.
+// MSGL_PREFILL_DMA_BUILTIN=1 builds the builtin form instead.
+#ifndef MSGL_PREFILL_DMA_BUILTIN
+#define MSGL_PREFILL_DMA_BUILTIN 0
+#endif
 __device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
-  // m0 is reserved by the compiler, so it cannot be listed as clobbered; the
-  // kernels using this helper have no other m0 user.
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(g), "s"(lds_addr) : "memory");
+#if MSGL_PREFILL_DMA_BUILTIN
+  __builtin_amdgcn_global_load_lds(g, (MSGL_LDS void*)(uintptr_t)lds_addr, 16, 0, 0);
+#else
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds_addr)
+      : "memory");
+#endif
 }
 
 // The value of lane l ^ 32 combined with this lane's, on the VALU:
@@ -135,9 +169,22 @@ __device__ __forceinline__ float xor32_sum(float x) {
   return h[0] + h[1];
 }
 
-// 4 bytes per active lane from global memory into LDS at m0 + 4 * lane.
+// 4 bytes per active lane (see dma16).
 __device__ __forceinline__ void dma4(const void* g, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(lds_addr) : "memory");
+#if MSGL_PREFILL_DMA_BUILTIN
+  __builtin_amdgcn_global_load_lds(g, (MSGL_LDS void*)(uintptr_t)lds_addr, 4, 0, 0);
+#else
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds_addr)
+      : "memory");
+#endif
 }
 
 // ds_read_b64_tr_b8: within each 16-lane group, lane i receives byte i%8 of
@@ -287,7 +334,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
   const uint32_t lds0 = (uint32_t)(uintptr_t)((MSGL_LDS uint8_t*)smem);
 
   // ---- work item from the plan (workgroups past its end have nothing to do) ----
-  if (wg >= *p.plan_count) return;
+  if (wg >= *p.plan_count || !plan_matches(p)) return;
   const int4 item = p.plan[2 * wg];
   const int4 geo = p.plan[2 * wg + 1];  // the request's geometry, loaded with the item
   const int kvh = item.y, qblk = item.z, split = item.w;
@@ -318,11 +365,12 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
   const int my_tok = min(qb + my_row / G, E - 1);
   const int limit = P + my_tok;
   const int lim_lo = __builtin_amdgcn_readfirstlane(limit);  // the wavefront's first row (lane 0)
-  // Q fragment (B operand of S^T = K Q^T): d = 16j + 8h .. +7
+  // Q fragment (B operand of S^T = K Q^T): d = 16j + 8h .. +7 (rows clamped
+  // into [0, num_tokens): q holds num_tokens rows whatever the offsets say)
   u32x4 qf[NQF];
   {
-    const uint8_t* qrow =
-        reinterpret_cast<const uint8_t*>(p.q) + ((int64_t)(q0 + my_tok) * p.hq + kvh * G + my_row % G) * D * 2;
+    const int64_t qr = min((int64_t)max(q0 + my_tok, 0), (int64_t)p.num_tokens - 1);
+    const uint8_t* qrow = reinterpret_cast<const uint8_t*>(p.q) + (qr * p.hq + kvh * G + my_row % G) * D * 2;
 #pragma unroll
     for (int j = 0; j < NQF; ++j) qf[j] = ld16(qrow + (16 * j + 8 * h) * 2);
   }
@@ -338,6 +386,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
   const uint8_t* vp = reinterpret_cast<const uint8_t*>(p.v_pool);
   const int64_t row_stride = (int64_t)p.hkv * RBYTES;
   const int64_t head_off = (int64_t)kvh * RBYTES;
+  const int64_t nidx = p.kv_indptr[p.num_reqs];  // entries of kv_indices
 
   // This wavefront's IPW transfers of each of K and V per tile. Transfer qi
   // covers LDS bytes [qi KiB, (qi+1) KiB) of the tile: lane l fills physical
@@ -642,7 +691,8 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
 #pragma unroll
       for (int k = 0; k < SPT; ++k) {  // kv_slot in two passes: every load before any use
         const int tok = w0 + min(tid + k * THREADS16, nw - 1);
-        sv[k] = p.kv_indices[kv_start + (p.page_size == 1 ? tok : tok / p.page_size)];
+        const int64_t ix = (int64_t)kv_start + (p.page_size == 1 ? tok : tok / p.page_size);
+        sv[k] = (ix >= 0 && ix < nidx) ? p.kv_indices[ix] : -1;  // -1: outside kv_indices, becomes slot 0
       }
 #pragma unroll
       for (int k = 0; k < SPT; ++k) {
@@ -751,7 +801,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       const int row = wave * 32 + m;
       const int tok = qb + row / G;
       const float rinv = __shfl(inv, m);
-      if (tok < E) {
+      if (tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {
         T* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) orow[32 * dt + rl] = from_f32<T>(acc[dt][i] * rinv);
@@ -761,14 +811,14 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
     const int64_t base = (int64_t)split * p.num_tokens;
     if (h == 0) {
       const int tok = qb + my_row / G;
-      if (tok < E && q0 + tok < p.num_tokens)
+      if (tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens)
         p.part_ml[(base + q0 + tok) * p.hq + kvh * G + my_row % G] = make_float2(m_run, l_row);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int row = wave * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
       const int tok = qb + row / G;
-      if (tok < E && q0 + tok < p.num_tokens) {  // the workspace holds num_tokens rows
+      if (tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {  // the workspace holds num_tokens rows
         float* orow = p.part_o + ((base + q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) orow[32 * dt + rl] = acc[dt][i];
@@ -787,7 +837,8 @@ template <typename T, int D>
 __device__ __forceinline__ void prefill_merge_body(const PrefillParams& p, int tk, int hy) {
   constexpr int TPH = D / 4;
   constexpr int HPB = 256 / TPH;
-  const int n = p.merge_n[tk];
+  if (!plan_matches(p)) return;
+  const int n = min(p.merge_n[tk], p.splits);
   if (n <= 1) return;  // written by the attention kernel (or not a token of any request)
   const int h = hy * HPB + threadIdx.x / TPH;
   const int d = (threadIdx.x % TPH) * 4;

@@ -139,6 +139,35 @@ SIGNATURES["msgl_mixed_attention"] = (
      _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32, _c_f, _c_p],
 )
 
+SIGNATURES["msgl_paged_decode_planned_ex"] = (
+    ctypes.c_int,
+    [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,  # q, k_new, v_new, out_loc, k_pool, v_pool, kv_scale
+     _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32,
+     _c_f, _c_i32, ctypes.c_uint32, _c_p, _c_p, _c_i64, _c_p],
+)
+SIGNATURES["msgl_paged_decode_merge"] = (
+    ctypes.c_int,
+    [_c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_i64, _c_p],
+)
+MSGL_DECODE_NO_MERGE = 1
+
+SIGNATURES["msgl_profile_next_launch"] = (ctypes.c_int, [_c_p, _c_p])
+
+SIGNATURES["msgl_validate_metadata"] = (
+    ctypes.c_int,
+    [_c_p, _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i64, _c_i64, _c_i32, _c_p, _c_p],
+)
+
+# msgl_meta_error codes of msgl_validate_metadata
+META_ERRORS = {
+    1: "kv_indptr is negative or decreasing",
+    2: "kv_indptr[R] lies beyond the entries of kv_indices",
+    3: "a sequence length is negative or needs more index entries than its kv_indptr row holds",
+    4: "an index entry names a slot (page) outside the pool",
+    5: "q_indptr does not run from 0 to num_tokens without decreasing",
+    6: "an extend length exceeds its sequence length",
+}
+
 _lib = None
 
 

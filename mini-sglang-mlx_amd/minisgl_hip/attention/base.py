@@ -50,17 +50,29 @@ class BaseAttnBackend(ABC):
     # ------------------------------------------------------------------ interface
 
     def prepare_metadata(self, batch: "Batch") -> None:
-        """attention/base.py:49-54: host-side index preparation before forward."""
-        if batch.is_prefill:
+        """attention/base.py:49-54: host-side index preparation before forward.
+        A ``"mixed"`` batch (decode requests first, then prefill chunks; the
+        reference never forms one) goes to ``prepare_mixed``."""
+        if batch.phase == "mixed":
+            batch.attn_metadata = self.prepare_mixed(batch)
+        elif batch.is_prefill:
             batch.attn_metadata = self._prepare_prefill(batch)
         else:
             batch.attn_metadata = self.prepare_decode(batch)
 
     def forward(self, q, k, v, layer_id: int, batch: "Batch"):
         """attention/base.py:56-60. q [T, Hq, D], k/v [T, Hkv, D] (already stored) -> o [T, Hq, D]."""
+        if batch.phase == "mixed":
+            return self.forward_mixed(q, k, v, layer_id, batch.attn_metadata)
         if batch.is_prefill:
             return self._forward_prefill(q, k, v, layer_id, batch.attn_metadata)
         return self.forward_decode(q, layer_id, batch.attn_metadata)
+
+    def prepare_mixed(self, batch: "Batch"):
+        raise NotImplementedError(f"{type(self).__name__} runs one phase per batch (attention/base.py:49-60)")
+
+    def forward_mixed(self, q, k, v, layer_id: int, metadata):
+        raise NotImplementedError(f"{type(self).__name__} runs one phase per batch (attention/base.py:49-60)")
 
     @abstractmethod
     def prepare_decode(self, batch: "Batch"): ...

@@ -43,10 +43,14 @@ class Req:
 
 @dataclass
 class Batch:
-    """core.py:99-120. ``positions``/``out_loc`` are filled by the caller, ``attn_metadata`` by the backend."""
+    """core.py:99-120. ``positions``/``out_loc`` are filled by the caller, ``attn_metadata`` by the backend.
+
+    ``phase`` ``"mixed"`` (not formed by the reference, whose batches hold one
+    phase, core.py:102): decode requests (one new token each) first, then
+    prefill chunks, run as one continuous-batching step."""
 
     reqs: List[Req]
-    phase: Literal["prefill", "decode"]
+    phase: Literal["prefill", "decode", "mixed"]
     input_ids: Any = field(default=None, init=False)
     positions: Any = field(default=None, init=False)
     out_loc: Any = field(default=None, init=False)

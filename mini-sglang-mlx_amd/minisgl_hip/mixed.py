@@ -29,26 +29,28 @@ from __future__ import annotations
 
 from typing import Optional
 
+import numpy as np
 import torch
 
 from . import ops
 
 
 class MixedStep:
-    """Device copies of a step's per-request arrays plus reusable workspaces."""
+    """Device copies of a step's per-request arrays plus reusable workspaces.
+
+    ``table_idx``, ``cached_len`` and ``device_len`` are the scheduler's host
+    arrays (one entry per request, decode requests first); the output sizes of
+    the index build (tokens, index entries, longest chunk and sequence) are
+    derived from them, so they always fit the indices the GPU builds."""
 
     def __init__(
         self,
         req_to_token: torch.Tensor,
-        table_idx: torch.Tensor,
-        cached_len: torch.Tensor,
-        device_len: torch.Tensor,
+        table_idx,
+        cached_len,
+        device_len,
         *,
         num_decode: int,
-        num_tokens: int,
-        num_pages: int,
-        max_chunk: int,
-        max_seq_len: int,
         num_qo_heads: int,
         num_kv_heads: int,
         head_dim: int,
@@ -56,19 +58,33 @@ class MixedStep:
         decode_splits: Optional[int] = None,
         prefill_splits: Optional[int] = None,
     ) -> None:
-        self.req_to_token = req_to_token
-        self.table_idx = table_idx
-        self.cached_len = cached_len
-        self.device_len = device_len
-        self.num_decode = num_decode
-        self.num_tokens = num_tokens
-        self.num_pages = num_pages
-        self.max_chunk = max_chunk
-        self.max_seq_len = max_seq_len
-        self.page_size = page_size
-        num_reqs = table_idx.shape[0]
-        num_prefill = num_reqs - num_decode
         dev = req_to_token.device
+        table_idx = np.asarray(table_idx, dtype=np.int32)
+        cached = np.asarray(cached_len, dtype=np.int32)
+        lens = np.asarray(device_len, dtype=np.int32)
+        if not (table_idx.shape == cached.shape == lens.shape) or table_idx.ndim != 1:
+            raise ValueError("table_idx, cached_len and device_len must be [R] host arrays")
+        ext = lens.astype(np.int64) - cached
+        if (ext < 1).any() or (cached < 0).any():
+            raise ValueError("every request must extend by at least one token")
+        if not 0 <= num_decode <= len(lens) or (ext[:num_decode] != 1).any():
+            raise ValueError("the first num_decode requests must extend by exactly one token")
+        self.req_to_token = req_to_token
+        self.table_idx = torch.from_numpy(table_idx).to(dev)
+        self.cached_len = torch.from_numpy(cached).to(dev)
+        self.device_len = torch.from_numpy(lens).to(dev)
+        self.num_decode = num_decode
+        self.num_tokens = int(ext.sum())
+        self.num_pages = int(((lens.astype(np.int64) + page_size - 1) // page_size).sum())
+        self.max_chunk = int(ext[num_decode:].max()) if num_decode < len(lens) else 0
+        self.max_seq_len = int(lens.max())
+        self.page_size = page_size
+        self._host_lens = (cached, lens)
+        num_reqs = len(lens)
+        num_prefill = num_reqs - num_decode
+        max_seq_len = self.max_seq_len
+        max_chunk = self.max_chunk
+        num_tokens = self.num_tokens
         if decode_splits is None:
             decode_splits = ops.default_splits(max(num_decode, 1), num_kv_heads, max_seq_len)
         if prefill_splits is None:
@@ -93,7 +109,7 @@ class MixedStep:
     def build_indices(self) -> dict:
         self.indices = ops.build_step_indices(
             self.req_to_token, self.table_idx, self.cached_len, self.device_len,
-            num_tokens=self.num_tokens, num_kv=self.num_pages, page_size=self.page_size,
+            num_tokens=self.num_tokens, num_kv=self.num_pages, page_size=self.page_size, host_lens=self._host_lens,
         )
         return self.indices
 

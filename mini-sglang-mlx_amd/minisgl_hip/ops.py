@@ -8,6 +8,7 @@ reference's asserts (attention/metal.py:122); kernel/runtime failures raise
 
 from __future__ import annotations
 
+import weakref
 from typing import Optional, Union
 
 import torch
@@ -28,6 +29,31 @@ def _check_index(name: str, t: Optional[torch.Tensor], device: torch.device) -> 
     if t.dtype != torch.int32:
         raise ValueError(f"{name} must be int32 (got {t.dtype})")
     _check_device(name, t, device)
+
+
+# id(tensor) -> (weak reference, tensor version, value) of device scales already read
+_SCALE_CACHE: dict = {}
+
+
+def scale_value(scale: Union[float, torch.Tensor]) -> float:
+    """The softmax scale as a float. The reference passes it as a one-element
+    array (attention/metal.py:143); a device tensor is read once (one host
+    sync) and the value is reused for as long as that tensor is alive and
+    unchanged (its version counter), so layers that share a scale tensor do not
+    synchronise per call."""
+    if not isinstance(scale, torch.Tensor):
+        return float(scale)
+    if scale.numel() != 1:
+        raise ValueError(f"scale must have one element (got shape {tuple(scale.shape)})")
+    if scale.device.type == "cpu":
+        return float(scale.reshape(-1)[0])
+    hit = _SCALE_CACHE.get(id(scale))
+    if hit is not None and hit[0]() is scale and hit[1] == scale._version:
+        return hit[2]
+    value = float(scale.reshape(-1)[0].item())
+    key = id(scale)
+    _SCALE_CACHE[key] = (weakref.ref(scale, lambda _r, k=key: _SCALE_CACHE.pop(k, None)), scale._version, value)
+    return value
 
 
 def store_kv(
@@ -148,11 +174,15 @@ def paged_decode_plan(
     dev = workspace.device
     _check_index("kv_indptr", kv_indptr, dev)
     _check_index("seq_lens", seq_lens, dev)
+    if kv_indptr.dim() != 1 or kv_indptr.shape[0] < batch + 1:
+        raise ValueError("kv_indptr must be [B+1]")
     status = _lib.load().msgl_paged_decode_plan(
         _lib.ptr(kv_indptr), _lib.ptr(seq_lens), batch, num_qo_heads, num_kv_heads, head_dim, max_splits,
         _lib.ptr(workspace), workspace.numel() * workspace.element_size(), _lib.current_stream(dev),
     )
     _lib.check(status, "msgl_paged_decode_plan")
+    # the sizes this plan is for: a planned call with other sizes is rejected
+    workspace._msgl_decode_plan = (batch, num_kv_heads, max_splits)
 
 
 def paged_decode_attention(
@@ -172,8 +202,14 @@ def paged_decode_attention(
     new_kv: Optional[tuple] = None,
     planned: bool = False,
     kv_scale: Optional[torch.Tensor] = None,
+    merge: bool = True,
 ) -> torch.Tensor:
     """Paged decode attention; counterpart of attention/metal.py:112-131.
+
+    ``merge=False`` (with ``planned``) launches the decode kernel only; the
+    rows of requests cut into several chunks are then completed by
+    ``paged_decode_merge`` with the same arguments (msgl_paged_decode_planned_ex
+    with MSGL_DECODE_NO_MERGE, then msgl_paged_decode_merge).
 
     fp8 pools (``torch.float8_e4m3fn``, written by ``store_kv_fp8``) take
     ``kv_scale`` (float32 [N, Hkv, 2]: K scale, V scale); q is bf16/fp16 and the
@@ -209,15 +245,14 @@ def paged_decode_attention(
         raise ValueError("q and pools must share one dtype")
     if page_size > 1 and seq_lens is None:
         raise ValueError("page_size > 1 needs seq_lens")
-    if kv_indptr.dim() != 1 or kv_indptr.shape[0] < b + (0 if seq_lens is not None else 1):
-        raise ValueError("kv_indptr must be [B+1]")
+    if kv_indptr.dim() != 1 or kv_indptr.shape[0] < b + 1:
+        raise ValueError("kv_indptr must be [B+1] (kv_indptr[B] = entries of kv_indices)")
     dev = q.device
     for name, t in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
         _check_device(name, t, dev)
     for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices), ("seq_lens", seq_lens)):
         _check_index(name, t, dev)
-    if isinstance(scale, torch.Tensor):
-        scale = float(scale.reshape(-1)[0].item())
+    scale = scale_value(scale)
     if out is None:
         out = torch.empty_like(q)
     else:
@@ -232,12 +267,36 @@ def paged_decode_attention(
         if planned:
             raise ValueError("planned decode needs the workspace its plan was built in")
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    if planned and getattr(workspace, "_msgl_decode_plan", None) != (b, hkv, max_splits):
+        raise ValueError(
+            f"planned decode: the workspace holds no plan for batch {b}, {hkv} kv heads, max_splits {max_splits} "
+            f"(plan: {getattr(workspace, '_msgl_decode_plan', None)})"
+        )
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     common = (
         _lib.ptr(kv_indptr), _lib.ptr(kv_indices), _lib.ptr(seq_lens),
         b, hq, hkv, d, page_size, n_slots, _lib.dtype_code(q.dtype), float(scale),
         max_splits, _lib.ptr(out), _lib.ptr(workspace), ws_bytes, _lib.current_stream(dev),
     )
+    if not merge:
+        if not planned:
+            raise ValueError("merge=False needs a planned call (the merge reads the plan)")
+        k_new = v_new = out_loc = None
+        if new_kv is not None:
+            k_new, v_new, out_loc = new_kv
+            if k_new.shape != (b, hkv, d) or v_new.shape != (b, hkv, d) or out_loc.shape != (b,):
+                raise ValueError("k_new/v_new must be [B, Hkv, D] and out_loc [B]")
+            if k_new.dtype != q.dtype or v_new.dtype != q.dtype:
+                raise ValueError("k_new/v_new must share q's dtype")
+            for name, t in (("k_new", k_new), ("v_new", v_new)):
+                _check_device(name, t, dev)
+            _check_index("out_loc", out_loc, dev)
+        status = lib.msgl_paged_decode_planned_ex(
+            _lib.ptr(q), _lib.ptr(k_new), _lib.ptr(v_new), _lib.ptr(out_loc), _lib.ptr(k_pool), _lib.ptr(v_pool),
+            _lib.ptr(kv_scale), *common[:12], _lib.MSGL_DECODE_NO_MERGE, *common[12:],
+        )
+        _lib.check(status, "msgl_paged_decode_planned_ex")
+        return out
     if fp8 and new_kv is None:
         fn = lib.msgl_paged_decode_fp8_planned if planned else lib.msgl_paged_decode_fp8
         status = fn(_lib.ptr(q), _lib.ptr(k_pool), _lib.ptr(v_pool), _lib.ptr(kv_scale), *common)
@@ -269,6 +328,32 @@ def paged_decode_attention(
                 *common,
             )
             _lib.check(status, "msgl_paged_decode_store")
+    return out
+
+
+def paged_decode_merge(
+    out: torch.Tensor,
+    kv_indptr: torch.Tensor,
+    seq_lens: Optional[torch.Tensor],
+    num_kv_heads: int,
+    max_splits: int,
+    workspace: torch.Tensor,
+) -> torch.Tensor:
+    """The split-K merge of a ``paged_decode_attention(..., planned=True,
+    merge=False)`` call with the same indices, sizes and workspace: completes
+    ``out`` [B, Hq, D] in place (msgl_paged_decode_merge)."""
+    b, hq, d = out.shape
+    dev = out.device
+    _check_device("out", out, dev)
+    _check_index("kv_indptr", kv_indptr, dev)
+    _check_index("seq_lens", seq_lens, dev)
+    if getattr(workspace, "_msgl_decode_plan", None) != (b, num_kv_heads, max_splits):
+        raise ValueError("paged_decode_merge: the workspace holds no plan for these sizes")
+    status = _lib.load().msgl_paged_decode_merge(
+        _lib.ptr(kv_indptr), _lib.ptr(seq_lens), b, hq, num_kv_heads, d, _lib.dtype_code(out.dtype), int(max_splits),
+        _lib.ptr(out), _lib.ptr(workspace), workspace.numel() * workspace.element_size(), _lib.current_stream(dev),
+    )
+    _lib.check(status, "msgl_paged_decode_merge")
     return out
 
 
@@ -326,14 +411,15 @@ def prefill_ragged_attention(
     if q_indptr.dim() != 1 or q_indptr.shape[0] < 2:
         raise ValueError("q_indptr must be [R+1]")
     num_reqs = q_indptr.shape[0] - 1
+    if kv_indptr.dim() != 1 or kv_indptr.shape[0] < num_reqs + 1:
+        raise ValueError("kv_indptr must be [R+1] (kv_indptr[R] = entries of kv_indices)")
     dev = q.device
     for name, x in (("q", q), ("k_pool", k_pool), ("v_pool", v_pool)):
         _check_device(name, x, dev)
     for name, x in (("q_indptr", q_indptr), ("kv_indptr", kv_indptr), ("kv_indices", kv_indices),
                     ("seq_lens", seq_lens)):
         _check_index(name, x, dev)
-    if isinstance(scale, torch.Tensor):
-        scale = float(scale.reshape(-1)[0].item())
+    scale = scale_value(scale)
     if out is None:
         out = torch.empty_like(q)
     else:
@@ -351,6 +437,12 @@ def prefill_ragged_attention(
         if planned:
             raise ValueError("planned prefill needs the workspace its plan was built in")
         workspace = torch.empty(need, dtype=torch.uint8, device=dev)
+    plan_key = (num_reqs, t, int(max_extend_len), int(max_seq_len), hq, hkv, d, int(max_splits))
+    if planned and need > 0 and getattr(workspace, "_msgl_prefill_plan", None) != plan_key:
+        raise ValueError(
+            f"planned prefill: the workspace holds no plan for {plan_key} "
+            f"(plan: {getattr(workspace, '_msgl_prefill_plan', None)})"
+        )
     ws_bytes = 0 if workspace is None else workspace.numel() * workspace.element_size()
     if fp8:
         fn = lib.msgl_prefill_ragged_fp8_planned if planned else lib.msgl_prefill_ragged_fp8
@@ -389,12 +481,16 @@ def prefill_plan(
     dev = workspace.device
     for name, x in (("q_indptr", q_indptr), ("kv_indptr", kv_indptr), ("seq_lens", seq_lens)):
         _check_index(name, x, dev)
+    if kv_indptr.dim() != 1 or kv_indptr.shape[0] < q_indptr.shape[0]:
+        raise ValueError("kv_indptr must be [R+1]")
     status = _lib.load().msgl_prefill_plan(
         _lib.ptr(q_indptr), _lib.ptr(kv_indptr), _lib.ptr(seq_lens), q_indptr.shape[0] - 1, int(num_tokens),
         int(max_extend_len), int(max_seq_len), num_qo_heads, num_kv_heads, head_dim, _lib.dtype_code(dtype),
         int(max_splits), _lib.ptr(workspace), workspace.numel() * workspace.element_size(), _lib.current_stream(dev),
     )
     _lib.check(status, "msgl_prefill_plan")
+    workspace._msgl_prefill_plan = (q_indptr.shape[0] - 1, int(num_tokens), int(max_extend_len), int(max_seq_len),
+                                    num_qo_heads, num_kv_heads, head_dim, int(max_splits))
 
 
 def mixed_attention(
@@ -449,6 +545,12 @@ def mixed_attention(
         out = torch.empty_like(q)
     elif out.shape != q.shape or out.dtype != q.dtype:
         raise ValueError("out must match q's shape and dtype")
+    num_prefill = q_indptr.shape[0] - 1
+    if num_decode and getattr(dec_workspace, "_msgl_decode_plan", None) != (num_decode, hkv, int(dec_max_splits)):
+        raise ValueError("mixed attention: dec_workspace holds no decode plan for these sizes")
+    pf_key = (num_prefill, t, int(max_extend_len), int(max_seq_len), hq, hkv, d, int(pf_max_splits))
+    if num_prefill and getattr(pf_workspace, "_msgl_prefill_plan", None) != pf_key:
+        raise ValueError("mixed attention: pf_workspace holds no prefill plan for these sizes")
     k_new = v_new = out_loc = None
     if new_kv is not None:
         k_new, v_new, out_loc = new_kv
@@ -482,6 +584,7 @@ def build_step_indices(
     num_tokens: int,
     num_kv: int,
     page_size: int = 1,
+    host_lens: Optional[tuple] = None,
 ) -> dict:
     """Step metadata built on the GPU from a device page table.
 
@@ -490,8 +593,12 @@ def build_step_indices(
     attention/metal.py:145-152 (kv_indptr, kv_indices; page ids of
     ceil(L / page_size) pages when page_size > 1). ``num_tokens`` =
     sum(device_len - cached_len) and ``num_kv`` = sum of (page-)lengths are
-    host-known sizes of the outputs. Returns device int32 tensors.
+    host-known sizes of the outputs; ``host_lens`` = (cached_len, device_len)
+    host arrays checks them first (``check_step_sizes``). Returns device int32
+    tensors.
     """
+    if host_lens is not None:
+        check_step_sizes(host_lens[0], host_lens[1], page_size, num_tokens, num_kv)
     if req_to_token.dim() != 2:
         raise ValueError("req_to_token must be [rows, max_seq_len]")
     r = table_idx.shape[0]
@@ -523,6 +630,80 @@ def build_step_indices(
     )
     _lib.check(status, "msgl_build_step_indices")
     return out
+
+
+def profile_next_launch(start: Optional["torch.cuda.Event"], stop: Optional["torch.cuda.Event"]) -> None:
+    """Arm this thread's next main-kernel launch (decode, decode merge, prefill
+    or mixed kernel) to record ``start``/``stop`` (timing events) at its own
+    dispatch start and end (msgl_profile_next_launch); ``stop`` then
+    ``start.elapsed_time(stop)`` is that kernel's duration. None, None disarms."""
+    handles = []
+    for e in (start, stop):
+        if e is None:
+            handles.append(None)
+            continue
+        if not e.cuda_event:  # torch creates the event at its first record
+            e.record()
+        handles.append(e.cuda_event)
+    _lib.check(_lib.load().msgl_profile_next_launch(*handles), "msgl_profile_next_launch")
+
+
+def validate_metadata(
+    kv_indptr: torch.Tensor,
+    kv_indices: torch.Tensor,
+    seq_lens: Optional[torch.Tensor],
+    *,
+    num_slots: int,
+    page_size: int = 1,
+    q_indptr: Optional[torch.Tensor] = None,
+    num_tokens: int = 0,
+) -> None:
+    """Check a decode (``q_indptr`` None) or prefill call's index metadata on
+    the device and raise ``ValueError`` naming the first violation found
+    (``msgl_validate_metadata``); the counterpart of the reference's
+    precondition asserts (attention/metal.py:122). Synchronises once to read the
+    result, so it is opt-in."""
+    dev = kv_indptr.device
+    for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices), ("seq_lens", seq_lens),
+                    ("q_indptr", q_indptr)):
+        _check_index(name, t, dev)
+    if kv_indptr.dim() != 1 or kv_indptr.shape[0] < 1:
+        raise ValueError("kv_indptr must be [R+1]")
+    r = kv_indptr.shape[0] - 1
+    if seq_lens is not None and seq_lens.shape[0] < r:
+        raise ValueError("seq_lens must be [R]")
+    if q_indptr is not None and q_indptr.shape[0] < r + 1:
+        raise ValueError("q_indptr must be [R+1]")
+    status = torch.empty(3, dtype=torch.int64, device=dev)
+    st = _lib.load().msgl_validate_metadata(
+        _lib.ptr(kv_indptr), _lib.ptr(kv_indices), _lib.ptr(seq_lens), _lib.ptr(q_indptr), r, int(page_size),
+        kv_indices.numel(), int(num_slots), int(num_tokens), _lib.ptr(status), _lib.current_stream(dev),
+    )
+    _lib.check(st, "msgl_validate_metadata")
+    code, where, value = status.tolist()
+    if code != 0:
+        what = _lib.META_ERRORS.get(code, f"error {code}")
+        raise ValueError(f"invalid attention metadata: {what} (at {where}: {value})")
+
+
+def check_step_sizes(cached_len, device_len, page_size: int, num_tokens: int, num_kv: int) -> None:
+    """Host-side check of the output sizes given to ``build_step_indices``
+    against the host copies of the step's lengths: the builder stops writing
+    at its capacities, so a short capacity would leave the attention launches
+    with fewer index entries than the offsets describe."""
+    import numpy as np
+
+    c = np.asarray(cached_len, dtype=np.int64)
+    d = np.asarray(device_len, dtype=np.int64)
+    if c.shape != d.shape:
+        raise ValueError("cached_len and device_len must have one length")
+    need_t = int(np.maximum(d - c, 0).sum())
+    lens = np.maximum(d, 0)
+    need_kv = int(lens.sum() if page_size == 1 else ((lens + page_size - 1) // page_size).sum())
+    if num_tokens != need_t:
+        raise ValueError(f"num_tokens is {num_tokens}, the step extends {need_t} tokens")
+    if num_kv != need_kv:
+        raise ValueError(f"num_kv is {num_kv}, the step's requests hold {need_kv} index entries")
 
 
 def table_scatter(req_to_token: torch.Tensor, rows: torch.Tensor, cols: torch.Tensor, values: torch.Tensor) -> None:

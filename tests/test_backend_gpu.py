@@ -156,3 +156,80 @@ def test_fused_and_eager_store_agree(cuda_device):
         pools.append(torch.stack([kv.k_cache(0), kv.v_cache(0), kv.k_cache(1), kv.v_cache(1)]))
     assert torch.equal(outs[0], outs[1])
     assert torch.equal(pools[0].view(torch.int16), pools[1].view(torch.int16))
+
+
+def test_mixed_batch_through_backend(cuda_device):
+    """A continuous-batching step (4 decode requests, then a chunk over a cached
+    prefix and a fresh prompt) as one batch of phase "mixed" through
+    prepare_metadata / store_kv / forward (msgl_mixed_attention), then a decode
+    step of all six: every request vs the oracle, new rows at out_loc."""
+    dt = torch.bfloat16
+    cfg = ModelConfig(num_qo_heads=32, num_kv_heads=8, head_dim=128, num_layers=2)
+    kv = MHAKVCache(2, 16384, 8, 128, dt, cuda_device)
+    table = np.zeros((10, 2048), dtype=np.int32)
+    backend = create_attention_backend("hip", cfg, kv, table)
+    free = np.random.default_rng(4).permutation(16384).astype(np.int32)
+    hist = [90, 700, 33, 1500]
+    reqs = [Req(input_ids=np.zeros(n + 1, np.int32), table_idx=i, cached_len=n) for i, n in enumerate(hist)]
+    free = oracle.allocate_paged(table, free, [0, 1, 2, 3], [0] * 4, hist, 1)
+    reqs.append(Req(input_ids=np.zeros(300, np.int32), table_idx=7, cached_len=200))  # chunk over a cached prefix
+    free = oracle.allocate_paged(table, free, [7], [0], [200], 1)
+    reqs.append(Req(input_ids=np.zeros(77, np.int32), table_idx=9, cached_len=0))  # a fresh prompt
+    for layer in range(2):
+        kv.k[layer].copy_(randn(kv.k[layer].shape, 90 + layer, dt).to(cuda_device))
+        kv.v[layer].copy_(randn(kv.v[layer].shape, 95 + layer, dt).to(cuda_device))
+    for phase in ("mixed", "decode"):
+        rows = [r.table_idx for r in reqs]
+        cached = [r.cached_len for r in reqs]
+        device = [r.device_len for r in reqs]
+        free = oracle.allocate_paged(table, free, rows, cached, device, 1)
+        pos, out_loc = oracle.prepare_batch_indices(table, rows, cached, device)
+        batch = Batch(reqs=reqs, phase=phase)
+        batch.positions = i32(pos, cuda_device)
+        batch.out_loc = i32(out_loc, cuda_device)
+        backend.prepare_metadata(batch)
+        if phase == "mixed":
+            assert batch.attn_metadata.num_decode == 4
+            q_off, last, _ = oracle.prefill_metadata(table, rows, cached, device)
+            assert np.array_equal(batch.attn_metadata.last_indices.cpu().numpy(), last)
+        t = len(out_loc)
+        for layer in range(2):
+            q = randn((t, 32, 128), 300 + layer, dt).to(cuda_device)
+            k = randn((t, 8, 128), 310 + layer, dt).to(cuda_device)
+            v = randn((t, 8, 128), 320 + layer, dt).to(cuda_device)
+            print(f"case backend {phase} layer={layer}", flush=True)
+            kv.store_kv(k, v, batch.out_loc, layer)
+            o = backend.forward(q, k, v, layer, batch)
+            torch.cuda.synchronize()
+            loc = batch.out_loc.long()
+            assert torch.equal(kv.k_cache(layer)[loc], k) and torch.equal(kv.v_cache(layer)[loc], v)
+            kp, vp = to_np64(kv.k[layer]), to_np64(kv.v[layer])
+            q_off, _, kvi = oracle.prefill_metadata(table, rows, cached, device)
+            # every request as a prefill of its extend rows over its whole context (a
+            # one-row extend attends like decode: attention/base.py:103, mask None)
+            ref = oracle.forward_prefill(to_np64(q), to_np64(k), to_np64(v), kp, vp, q_off, kvi, 128**-0.5)
+            assert_close(o, ref, dt, f"backend {phase} layer {layer}")
+        for r in reqs:
+            if r.extend_len == 1 or phase == "mixed":
+                r.complete_one()
+
+
+def test_backend_validation_rejects_slots_outside_the_pool(cuda_device):
+    """validate=True: the step's device-built indices are checked before use; a
+    page-table entry past the pool fails prepare_metadata with ValueError."""
+    dt = torch.bfloat16
+    cfg = ModelConfig(num_qo_heads=16, num_kv_heads=8, head_dim=128, num_layers=1)
+    kv = MHAKVCache(1, 4096, 8, 128, dt, cuda_device)
+    table = np.zeros((4, 512), dtype=np.int32)
+    backend = create_attention_backend("hip", cfg, kv, table)
+    backend.validate = True
+    free = np.random.default_rng(6).permutation(4096).astype(np.int32)
+    reqs = [Req(input_ids=np.zeros(n + 1, np.int32), table_idx=i, cached_len=n) for i, n in enumerate([30, 120])]
+    free = oracle.allocate_paged(table, free, [0, 1], [0, 0], [31, 121], 1)
+    batch = Batch(reqs=reqs, phase="decode")
+    print("case backend validate ok", flush=True)
+    backend.prepare_metadata(batch)  # valid
+    table[1, 50] = 4096  # one slot past the pool
+    backend._mirrored[:] = 0  # send the rows again
+    with pytest.raises(ValueError, match="outside the pool"):
+        backend.prepare_metadata(Batch(reqs=reqs, phase="decode"))

@@ -35,7 +35,7 @@ def test_every_declared_symbol_is_exported_and_bound():
 
 def test_abi_version_and_sizes():
     lib = _lib.load()
-    assert lib.msgl_abi_version() == 1
+    assert lib.msgl_abi_version() == 2
     up = lambda x: (x + 255) // 256 * 256  # noqa: E731
     # [meta | work list: B x splits x kv-head groups (8 heads / 4 per workgroup) int4 | key offsets (B + 1) i64 |
     #  partials]
@@ -193,6 +193,15 @@ def test_host_side_argument_errors():
     assert pf8(sc=nul) == _lib.MSGL_ERR_INVALID and "kv_scale" in _lib.last_error()
     assert pf8(dtype=0) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()
     assert pf8(d=96) == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
+    # metadata validation: (kv_indptr, kv_indices, seq_lens, q_indptr, R, page, num_indices, slots, T, status,
+    #                       stream)
+    va = lambda st=16, r=2, page=1, nidx=8, slots=100, ip=16: lib.msgl_validate_metadata(  # noqa: E731
+        ip, 16, nul, nul, r, page, nidx, slots, 0, st, nul)
+    assert va(st=nul) == _lib.MSGL_ERR_INVALID and "status" in _lib.last_error()
+    assert va(st=12) == _lib.MSGL_ERR_INVALID  # int64 words
+    assert va(page=0) == _lib.MSGL_ERR_INVALID
+    assert va(slots=0) == _lib.MSGL_ERR_INVALID
+    assert va(ip=nul) == _lib.MSGL_ERR_INVALID and "null" in _lib.last_error()
     # store_kv: zero tokens is a no-op; bad row size is unsupported
     assert lib.msgl_store_kv(nul, nul, nul, nul, nul, 0, 8, 128, 10, 1, nul) == _lib.MSGL_OK
     assert lib.msgl_store_kv(16, 16, 16, 16, 16, 4, 1, 3, 10, 1, nul) == _lib.MSGL_ERR_UNSUPPORTED
@@ -228,6 +237,9 @@ def test_python_wrapper_raises():
                                    torch.zeros(2, dtype=torch.int32), 0.1, kv_scale=sc)
     with pytest.raises(ValueError):  # rotary_dim / inv_freq mismatch
         ops.rope(k, torch.zeros(2, dtype=torch.int32), torch.zeros(16), 64)
+    with pytest.raises(ValueError):  # kv_indptr must hold B + 1 offsets, also with seq_lens
+        ops.paged_decode_attention(torch.zeros(2, 8, 64), pool, pool, torch.zeros(2, dtype=torch.int32),
+                                   torch.zeros(2, dtype=torch.int32), 0.1, seq_lens=torch.ones(2, dtype=torch.int32))
     with pytest.raises(ValueError):  # the KV cache takes the model dtype or fp8 only
         from minisgl_hip.kvcache import MHAKVCache
         MHAKVCache(1, 8, 4, 64, torch.bfloat16, "cpu", kv_dtype=torch.float16)

@@ -89,7 +89,9 @@ def test_table_rows_with_seq_lens(cuda_device):
     dt = torch.bfloat16
     c = workloads.decode_case_from_lens([5, 300, 77, 1], num_slots=4096, seed=12)
     stride = c.page_table.shape[1]
-    starts = (np.arange(4) * stride).astype(np.int32)
+    assert c.page_table.shape[0] == 4
+    # row starts, then the table's entry count (kv_indptr[B]: where index reads stop)
+    starts = (np.arange(5) * stride).astype(np.int32)
     kp, vp = _pools(4096, 8, 128, dt, 400, cuda_device)
     q = randn((4, 16, 128), 402, dt).to(cuda_device)
     print("case table-rows", flush=True)

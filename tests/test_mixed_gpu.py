@@ -18,12 +18,10 @@ HQ, HKV, D = 32, 8, 128
 SCALE = D**-0.5
 
 
-def _step(case, device, max_seq_len):
+def _step(case, device):
     return MixedStep(
-        i32(case.req_to_token, device), i32(case.table_idx, device), i32(case.cached_len, device),
-        i32(case.device_len, device), num_decode=case.num_decode, num_tokens=case.num_tokens,
-        num_pages=case.num_pages, max_chunk=case.max_chunk, max_seq_len=max_seq_len, num_qo_heads=HQ,
-        num_kv_heads=HKV, head_dim=D, page_size=case.page_size,
+        i32(case.req_to_token, device), case.table_idx, case.cached_len, case.device_len,
+        num_decode=case.num_decode, num_qo_heads=HQ, num_kv_heads=HKV, head_dim=D, page_size=case.page_size,
     )
 
 
@@ -68,7 +66,7 @@ def test_mixed_step_small(cuda_device):
     vn = randn((t, HKV, D), 64, dt).to(cuda_device)
     out = torch.empty_like(q)
     kp1, vp1 = kp.clone(), vp.clone()
-    step = _step(case, cuda_device, int(case.device_len.max()))
+    step = _step(case, cuda_device)
     step.run(q, kn, vn, kp, vp, out, SCALE, single_launch=False)  # two streams
     out1 = torch.empty_like(q)
     step.run(q, kn, vn, kp1, vp1, out1, SCALE, single_launch=True)
@@ -99,7 +97,7 @@ def test_mixed_step_full_size(cuda_device):
     kn = torch.randn((t, HKV, D), generator=g, device=cuda_device, dtype=dt)
     vn = torch.randn((t, HKV, D), generator=g, device=cuda_device, dtype=dt)
     out = torch.empty_like(q)
-    step = _step(case, cuda_device, int(case.device_len.max()))
+    step = _step(case, cuda_device)
     step.run(q, kn, vn, kp, vp, out, SCALE, single_launch=False)  # two streams
     out2 = torch.empty_like(q)
     step.run(q, kn, vn, kp, vp, out2, SCALE, single_launch=False)
@@ -141,11 +139,10 @@ def test_mixed_single_launch_shapes(cuda_device, hq, hkv, d, page):
         kn = randn((t, hkv, d), 83, dt).to(cuda_device)
         vn = randn((t, hkv, d), 84, dt).to(cuda_device)
         step = MixedStep(
-            i32(case.req_to_token, cuda_device), i32(case.table_idx, cuda_device), i32(case.cached_len, cuda_device),
-            i32(case.device_len, cuda_device), num_decode=case.num_decode, num_tokens=t, num_pages=case.num_pages,
-            max_chunk=case.max_chunk, max_seq_len=int(case.device_len.max()), num_qo_heads=hq, num_kv_heads=hkv,
-            head_dim=d, page_size=page,
+            i32(case.req_to_token, cuda_device), case.table_idx, case.cached_len, case.device_len,
+            num_decode=case.num_decode, num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, page_size=page,
         )
+        assert (step.num_tokens, step.num_pages, step.max_chunk) == (t, case.num_pages, case.max_chunk)
         kp1, vp1 = kp.clone(), vp.clone()
         a = torch.empty_like(q)
         step.run(q, kn, vn, kp, vp, a, d**-0.5, concurrent=False, single_launch=False)
