@@ -458,6 +458,26 @@ int msgl_mixed_attention(const void* q_dec, const void* k_new, const void* v_new
                          int32_t page_size, int64_t num_slots, int32_t dtype, float scale, void* stream);
 
 /*
+ * msgl_paged_decode_store without a workspace argument, for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc). No counterpart in the reference.
+ * The work list and split-K partials live in a device array the library holds
+ * on each device it runs on (MSGL_NOALLOC_WORKSPACE_BYTES, from the first call
+ * on that device until the process ends); sizes whose workspace
+ * (msgl_paged_decode_workspace_size) exceeds it are rejected with
+ * MSGL_ERR_WORKSPACE. The call allocates nothing. Every call on one device
+ * shares that array: calls that overlap in time on a device (other streams or
+ * threads) race; calls in order on one stream do not. Same arguments, results
+ * and pool contents as msgl_paged_decode_store.
+ */
+#define MSGL_NOALLOC_WORKSPACE_BYTES ((int64_t)32 << 20)
+int msgl_paged_decode_store_noalloc(const void* q, const void* k_new, const void* v_new, const int32_t* out_loc,
+                                    void* k_pool, void* v_pool, const int32_t* kv_indptr, const int32_t* kv_indices,
+                                    const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                    int32_t num_kv_heads, int32_t head_dim, int32_t page_size, int64_t num_slots,
+                                    int32_t dtype, float scale, int32_t max_splits, void* out, void* stream);
+
+/*
  * Instrumentation: the calling thread's next main-kernel launch -- the decode
  * kernel of a decode call, the merge of msgl_paged_decode_merge, the attention
  * kernel of a prefill call or the mixed-step kernel -- records start_event and

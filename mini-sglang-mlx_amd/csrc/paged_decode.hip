@@ -763,3 +763,83 @@ extern "C" int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* 
   return dispatch(MergeLaunch{p, batch, (hipStream_t)stream}, dtype, false, head_dim, num_qo_heads / num_kv_heads,
                   "msgl_paged_decode_merge");
 }
+
+// ---------------------------------------------------------------------------
+// Allocation-free decode: msgl_paged_decode_store with its workspace (the work
+// list and the split-K partials) in a file-scope device array instead of a
+// caller buffer. Each device holds its own copy of the array from the first
+// call on it until the process ends; its address on the current device comes
+// from hipGetSymbolAddress, looked up once per device (the array's name in
+// host code is only a host-side stand-in for it). Every call on a device uses
+// that device's one copy, so calls that overlap in time on one device (other
+// streams, other threads) race; calls in order on one stream do not. The
+// workspace needs no clearing: the plan kernel writes everything the decode
+// and merge kernels read.
+// ---------------------------------------------------------------------------
+namespace msgl {
+namespace {
+
+constexpr int64_t kNoAllocScratchBytes = MSGL_NOALLOC_WORKSPACE_BYTES;  // per device
+constexpr int kMaxDevices = 64;
+
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// The device address of `scratch` on the current device.
+int scratch_on_current_device(void** ptr) {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    set_error("msgl_paged_decode_store_noalloc: no usable current device");
+    return MSGL_ERR_HIP;
+  }
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    const hipError_t err = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || p == nullptr) {
+      set_error("msgl_paged_decode_store_noalloc: hipGetSymbolAddress failed: %s", hipGetErrorString(err));
+      return MSGL_ERR_HIP;
+    }
+    g_scratch_ptr[dev].store(p, std::memory_order_release);  // racing first calls store the same address
+  }
+  *ptr = p;
+  return MSGL_OK;
+}
+
+}  // namespace
+}  // namespace msgl
+
+extern "C" int msgl_paged_decode_store_noalloc(const void* q, const void* k_new, const void* v_new,
+                                               const int32_t* out_loc, void* k_pool, void* v_pool,
+                                               const int32_t* kv_indptr, const int32_t* kv_indices,
+                                               const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
+                                               int32_t num_kv_heads, int32_t head_dim, int32_t page_size,
+                                               int64_t num_slots, int32_t dtype, float scale, int32_t max_splits,
+                                               void* out, void* stream) {
+  using namespace msgl;
+  clear_error();
+  MSGL_CHECK_ARG(k_new && v_new && out_loc, "msgl_paged_decode_store_noalloc: null k_new, v_new or out_loc");
+  MSGL_CHECK_ARG(((uintptr_t)k_new | (uintptr_t)v_new) % 16 == 0,
+                 "msgl_paged_decode_store_noalloc: k_new and v_new must be 16-byte aligned");
+  MSGL_CHECK_ARG(batch >= 0 && batch <= 65535, "msgl_paged_decode_store_noalloc: batch must be in [0, 65535]");
+  if (batch == 0) return MSGL_OK;
+  MSGL_CHECK_ARG(num_qo_heads > 0 && num_kv_heads > 0 && head_dim > 0,
+                 "msgl_paged_decode_store_noalloc: sizes must be > 0");
+  int32_t splits = max_splits;
+  if (splits <= 0) splits = msgl_paged_decode_default_splits(batch, num_kv_heads, 0);
+  if (splits > kMaxSplits) splits = kMaxSplits;
+  const int64_t need = msgl_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, splits);
+  if (need > kNoAllocScratchBytes) {
+    set_error("msgl_paged_decode_store_noalloc: these sizes need %lld bytes of workspace, more than the %lld the "
+              "library holds per device (fewer max_splits or a smaller batch fit; msgl_paged_decode_store takes "
+              "any workspace)",
+              (long long)need, (long long)kNoAllocScratchBytes);
+    return MSGL_ERR_WORKSPACE;
+  }
+  void* ws = nullptr;
+  const int st = scratch_on_current_device(&ws);
+  if (st != MSGL_OK) return st;
+  return paged_decode_impl("msgl_paged_decode_store_noalloc", kPlanAndRun, q, k_new, v_new, out_loc, k_pool, v_pool,
+                           nullptr, kv_indptr, kv_indices, seq_lens, batch, num_qo_heads, num_kv_heads, head_dim,
+                           page_size, num_slots, dtype, scale, splits, out, ws, kNoAllocScratchBytes, stream);
+}

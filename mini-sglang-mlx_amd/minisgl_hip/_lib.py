@@ -152,6 +152,13 @@ SIGNATURES["msgl_paged_decode_merge"] = (
 MSGL_DECODE_NO_MERGE = 1
 
 SIGNATURES["msgl_profile_next_launch"] = (ctypes.c_int, [_c_p, _c_p])
+SIGNATURES["msgl_paged_decode_store_noalloc"] = (
+    ctypes.c_int,
+    [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p,  # q, k_new, v_new, out_loc, k_pool, v_pool
+     _c_p, _c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i64, _c_i32,
+     _c_f, _c_i32, _c_p, _c_p],  # scale, max_splits, out, stream
+)
+NOALLOC_WORKSPACE_BYTES = 32 << 20
 
 SIGNATURES["msgl_validate_metadata"] = (
     ctypes.c_int,
