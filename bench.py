@@ -257,7 +257,7 @@ def bench_decode(args, dev):
             ops.paged_decode_attention(qs[layer], kps[layer], vps[layer], indptr, indices, scale,
                                        max_splits=splits, out=outs[layer], workspace=ws,
                                        new_kv=(ks[layer], vs[layer], out_loc), planned=True, merge=False)
-            if layer == timed_layer:  # the merge kernel's
+            if layer == timed_layer and splits > 1:  # the merge kernel's (none when splits == 1)
                 ops.profile_next_launch(events[2], events[3])
             ops.paged_decode_merge(outs[layer], indptr, None, HKV, splits, ws)
 
@@ -276,7 +276,8 @@ def bench_decode(args, dev):
     # each kernel's own dispatch start to end (the span between them would also
     # hold the delay the timing events add in front of the next dispatch)
     kern_s = float(np.mean([e[0].elapsed_time(e[1]) for e in ev])) / 1e3  # decode kernel (store fused)
-    merge_s = float(np.mean([e[2].elapsed_time(e[3]) for e in ev])) / 1e3  # split-K merge kernel
+    merge_s = (float(np.mean([e[2].elapsed_time(e[3]) for e in ev])) / 1e3  # split-K merge kernel
+               if splits > 1 else 0.0)
     ms_per_step = elapsed / args.steps * 1e3
     value = step_bytes / (elapsed / args.steps) / 1e9
     achieved = (dec_bytes + store_bytes) / kern_s / 1e9  # the decode kernel alone
@@ -401,11 +402,13 @@ def bench_decode_fp8(args, dev):
             ops.paged_decode_attention(qs[layer], kp, vp, indptr, indices, D**-0.5, max_splits=splits,
                                        out=outs[layer], workspace=ws, planned=True, kv_scale=sc,
                                        new_kv=(ks[layer], vs[layer], out_loc), merge=False)
-            if ev and layer == timed:
+            if ev and layer == timed and splits > 1:
                 ops.profile_next_launch(ev[2], ev[3])
             ops.paged_decode_merge(outs[layer], indptr, None, HKV, splits, ws)
 
     sec, kern_s, merge_s = _timed(args, run, nev=4)
+    if splits == 1:
+        merge_s = 0.0
     ev_s = kern_s
     step_bytes = LAYERS * (dec_bytes + store_bytes)
     achieved = (dec_bytes + store_bytes) / ev_s / 1e9

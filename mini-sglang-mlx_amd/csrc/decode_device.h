@@ -149,6 +149,8 @@ struct DecodeParams {
   int hq, hkv, page_size, max_splits, batch, ngrp;
   bool planned;   // the workspace already holds this call's plan
   bool balanced;  // equal key ranges of the batch's token stream allowed (else per-request chunks)
+  bool shared_head;  // max_splits == 1: one (request, kv head) per 4-wavefront workgroup, tiles split over the waves
+  int hpg;           // kv heads per work-list group (the list's items are (request, group))
   bool skip_merge;  // host side: launch the decode kernel only (msgl_paged_decode_merge follows)
   float scale_log2;
 };
@@ -191,6 +193,13 @@ struct TileBuf {
 template <typename KV, int D>
 constexpr int k_lds_stride() { return D * (int)sizeof(KV) + 16; }
 
+// Dynamic LDS floats of a decode workgroup of nwaves wavefronts: the staged
+// slots, then per wave the P/alpha/(m, l) tiles and the K re-layout tile.
+template <typename KV, int D>
+__host__ __device__ constexpr int decode_lds_floats(int nwaves) {
+  return kSeg + kSlotPad + nwaves * (kLdsPerWave + 16 * k_lds_stride<KV, D>() / 4);
+}
+
 // Minimum wavefronts per SIMD the register allocator must allow (occupancy).
 #ifndef MSGL_DECODE_MIN_WAVES
 #define MSGL_DECODE_MIN_WAVES 2
@@ -203,11 +212,33 @@ constexpr int k_lds_stride() { return D * (int)sizeof(KV) + 16; }
 #define MSGL_DECODE_FP8_STAGES 2
 #endif
 
+// Tiles of K/V each wavefront holds in registers (its register budget; fp8
+// tiles are half the bytes, so they keep more in flight).
+template <typename T, typename KV, int D, int G>
+constexpr int decode_stages() {
+  return std::is_same<KV, fp8e4m3>::value ? (G <= 2 && D <= 128 ? MSGL_DECODE_FP8_STAGES : 2)
+                                          : ((sizeof(T) == 4 || D > 128 || G > 4) ? 2 : MSGL_DECODE_STAGES);
+}
+
+// The shared-head form (max_splits == 1): the 4 wavefronts of a workgroup take
+// every 4th tile of one (request, kv head) and combine their partial softmax
+// states in LDS, so the output is written by the one launch (no split-K
+// partials, no merge launch). Built where its strided prefetch fits the slot
+// padding (two register stages).
+constexpr int kSharedWaves = 4;
+template <typename T, typename KV, int D, int G>
+constexpr bool decode_shared() {
+  return (decode_stages<T, KV, D, G>() - 1) * kSharedWaves * 16 <= kSlotPad &&
+         (decode_lds_floats<KV, D>(kSharedWaves) + kSharedWaves * (G * D + 2 * G)) * 4 <= 65536;
+}
+
 // T: the query/output type; KV: the pool's storage type (T itself, or fp8e4m3
 // for a quantised pool with per-(slot, kv head) scales). RANGES: the key-range
 // form is built in (its chunk loop costs registers; without it every
-// workgroup runs one work-list item and p.balanced must be false).
-template <typename T, typename KV, int D, int G, bool RANGES>
+// workgroup runs one work-list item and p.balanced must be false). SHARED:
+// the shared-head form only (its own kernel, so the split forms keep their
+// register allocation).
+template <typename T, typename KV, int D, int G, bool RANGES, bool SHARED_FORM = false>
 __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg) {
   constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
   constexpr int VEC = QK<T>::VEC;   // query elements per 16-byte chunk (MFMA operand)
@@ -220,9 +251,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
   constexpr int R = 64 / LPR;       // K/V rows per wave load
   constexpr int NLV = 16 / R;       // K/V loads per lane per tile
   constexpr int NR = G < 4 ? G : 4; // MFMA accumulator rows holding query heads
-  // register budget; fp8 tiles are half the bytes, so they keep more in flight
-  constexpr int NST = Q8 ? (G <= 2 && D <= 128 ? MSGL_DECODE_FP8_STAGES : 2)
-                         : ((sizeof(T) == 4 || D > 128 || G > 4) ? 2 : MSGL_DECODE_STAGES);
+  constexpr int NST = decode_stages<T, KV, D, G>();
   static_assert(NST >= 2 && (NST - 1) * 16 <= kSlotPad, "pipeline depth");
   static_assert(D % KCHUNK == 0 && 64 % LPR == 0 && 16 % R == 0, "unsupported head_dim");
   static_assert(G >= 1 && G <= 16, "unsupported group size");
@@ -245,8 +274,14 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
 
   // One chunk: keys [t0, t1) of request b (L keys, kv_indices from start),
   // partial `split` of its n; the kv-head group kgrp is this workgroup's waves.
+  // Shared-head form (SHARED): kgrp is the one kv head of every wave, wave w
+  // takes tiles w, w + 4, ... of each segment, and the waves' partial states
+  // are combined in LDS into the output rows.
   auto run_chunk = [&](const int b, const int start, const int L, const int t0, const int t1, const int split,
-                       const int n, const int kgrp) {
+                       const int n, const int kgrp, auto shared_t) {
+  constexpr bool SHARED = decltype(shared_t)::value;
+  constexpr int TS = SHARED ? kSharedWaves : 1;  // tile stride of one wavefront
+  static_assert(!SHARED || (NST - 1) * TS * 16 <= kSlotPad, "strided prefetch past the slot padding");
   {
     // lane-derived indices are recomputed per chunk from an opaque copy of
     // the lane id: hoisted out of the chunk loop they would hold registers
@@ -257,7 +292,8 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
     const int g4 = lid >> 4;   // MFMA row group
     const int vc = lid % LPR;  // V: 16-byte chunk within the row
     const int vr = lid / LPR;  // V: token sub-row
-    const int kvh = kgrp * nwaves + wave;
+    const int kvh = SHARED ? kgrp : kgrp * nwaves + wave;
+    const int tile0 = SHARED ? wave : 0;  // this wavefront's first tile of a segment
     const bool active = kvh < p.hkv;
     const int kvh_c = active ? kvh : 0;
 
@@ -295,7 +331,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
     const int64_t new_off = ((int64_t)b * p.hkv + kvh_c) * D * ES + vc * VEC * ES;
     const uint8_t* knew_p = fused ? reinterpret_cast<const uint8_t*>(p.k_new) + new_off : nullptr;
     const uint8_t* vnew_p = fused ? reinterpret_cast<const uint8_t*>(p.v_new) + new_off : nullptr;
-    if (active && new_pos != 0x7fffffff && lane < LPR) {
+    if (active && new_pos != 0x7fffffff && lane < LPR && (!SHARED || wave == 0)) {
       const int64_t slot = p.out_loc[b];
       if (slot >= 0 && slot < p.num_slots) {
         const int64_t dst = slot * row_stride + (int64_t)kvh * D * ES + vc * VEC * ES;
@@ -337,7 +373,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
       // ---- stage this segment's slots, padded by NST-1 tiles; positions past
       //      the end repeat the last valid slot ----
       __syncthreads();
-      for (int i = threadIdx.x; i < (ntile + NST - 1) * 16; i += blockDim.x) {
+      for (int i = threadIdx.x; i < (ntile + (NST - 1) * TS) * 16; i += blockDim.x) {
         const int tok = s0 + min(i, seg_len - 1);
         slots_lds[i] = slot_of(p.kv_indices, nidx, start, tok, p.page_size, p.num_slots);
       }
@@ -426,17 +462,19 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
         }
       };
 
-      // NST-stage register pipeline: tiles t+1 .. t+NST-1 are in flight while t computes
+      // NST-stage register pipeline: this wavefront's next NST-1 tiles are in
+      // flight while one computes (tiles tile0, tile0 + TS, ...; past ntile: padding)
+      const int nloc = ntile > tile0 ? (ntile - tile0 + TS - 1) / TS : 0;
       TileBuf<KV, D> buf[NST];
 #pragma unroll
-      for (int i = 0; i < NST - 1; ++i) issue(buf[i], i);  // tiles past ntile are padding
-      for (int tile = 0; tile < ntile; tile += NST) {
+      for (int i = 0; i < NST - 1; ++i) issue(buf[i], tile0 + i * TS);
+      for (int j0 = 0; j0 < nloc; j0 += NST) {
 #pragma unroll
         for (int k = 0; k < NST; ++k) {
-          const int t = tile + k;
-          if (t >= ntile) break;
-          issue(buf[(k + NST - 1) % NST], t + NST - 1);
-          compute(buf[k], t);
+          const int j = j0 + k;
+          if (j >= nloc) break;
+          issue(buf[(k + NST - 1) % NST], tile0 + (j + NST - 1) * TS);
+          compute(buf[k], tile0 + j * TS);
         }
       }
     }
@@ -461,6 +499,40 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
     }
     wave_lds_sync();
     const int d0 = vc * VKV;
+    if constexpr (SHARED) {
+      // every wave's (acc, m, l) of the G heads into the combine region, then the
+      // workgroup folds the four: o = sum_w 2^(m_w - M) acc_w / sum_w 2^(m_w - M) l_w
+      constexpr int CW = G * D + 2 * G;  // floats per wave
+      float* comb = lds_all + decode_lds_floats<KV, D>(kSharedWaves);
+      float* mine = comb + wave * CW;
+      if (lane < LPR) {
+#pragma unroll
+        for (int g = 0; g < G; ++g)
+#pragma unroll
+          for (int e = 0; e < VKV; ++e) mine[g * D + d0 + e] = acc[g][e];
+      }
+      if (lane < G) {
+        mine[G * D + 2 * lane] = ML_lds[lane * 2 + 0];
+        mine[G * D + 2 * lane + 1] = ML_lds[lane * 2 + 1];
+      }
+      __syncthreads();
+      T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D;
+      for (int idx = threadIdx.x; idx < G * D; idx += kSharedWaves * 64) {
+        const int g = idx / D;
+        float M = -INFINITY;
+#pragma unroll
+        for (int w = 0; w < kSharedWaves; ++w) M = fmaxf(M, comb[w * CW + G * D + 2 * g]);
+        float num = 0.f, den = 0.f;
+#pragma unroll
+        for (int w = 0; w < kSharedWaves; ++w) {
+          const float f = __builtin_amdgcn_exp2f(comb[w * CW + G * D + 2 * g] - M);
+          num += f * comb[w * CW + idx];
+          den += f * comb[w * CW + G * D + 2 * g + 1];
+        }
+        o[idx] = from_f32<T>(num / den);
+      }
+      return;
+    }
     if (n == 1) {
       if (lane < LPR) {
         T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D + d0;
@@ -507,6 +579,26 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
   // is a chunk of its own, partial (k - the request's first range) of the
   // ranges it overlaps. Otherwise: one work item of the plan (workgroups past
   // its end have nothing to do).
+  if constexpr (SHARED_FORM) {
+    static_assert(decode_shared<T, KV, D, G>(), "no shared-head form for this instantiation");
+    {  // workgroup wg: head wg % hpg of the list's item wg / hpg
+      const int item_i = wg / p.hpg;
+      if (item_i >= p.meta[0] || !plan_matches(p)) return;
+      const int4 item = p.plan[item_i];
+      const int b = item.x;
+      const int head = item.z * p.hpg + wg % p.hpg;
+      if (head >= p.hkv) return;
+      const int start = p.kv_indptr[b];
+      const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - start;
+      if (L <= 0) {  // defined zero output for this head's query rows
+        T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + head * G) * D;
+        for (int i = threadIdx.x; i < G * D; i += blockDim.x) o[i] = from_f32<T>(0.f);
+        return;
+      }
+      run_chunk(b, start, L, 0, L, 0, 1, head, std::true_type{});
+      return;
+    }
+  }
   const bool bal = RANGES && balanced_launch(p);
   // the form this launch splits by, for the merge (which need not know the
   // kernel's residency or whether key ranges were built in)
@@ -569,7 +661,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
       n = (int)((ob1 - 1) / rl - ob / rl + 1);
       g0 = s1;
     }
-    run_chunk(b, start, L, t0, t1, split, n, kgrp);
+    run_chunk(b, start, L, t0, t1, split, n, kgrp, std::false_type{});
     if constexpr (!RANGES) return;
     if (!bal) return;
   }
@@ -658,10 +750,15 @@ __device__ __forceinline__ void paged_decode_merge_body(const DecodeParams& p, i
 #define MSGL_DECODE_WAVES_PER_WG 4
 #endif
 
-// Dynamic LDS of a decode workgroup of nwaves wavefronts.
+// Dynamic LDS bytes of a decode workgroup of nwaves wavefronts, and of a
+// shared-head workgroup (plus the region where its waves combine).
 template <typename KV, int D>
 inline size_t decode_lds_bytes(int nwaves) {
-  return ((size_t)kSeg + kSlotPad + (size_t)nwaves * (kLdsPerWave + 16 * k_lds_stride<KV, D>() / 4)) * sizeof(float);
+  return (size_t)decode_lds_floats<KV, D>(nwaves) * sizeof(float);
+}
+template <typename KV, int D, int G>
+inline size_t decode_shared_lds_bytes() {
+  return ((size_t)decode_lds_floats<KV, D>(kSharedWaves) + (size_t)kSharedWaves * (G * D + 2 * G)) * sizeof(float);
 }
 
 // Validates the arguments of a decode call and fills p (workspace regions

@@ -201,6 +201,7 @@ extern "C" int msgl_mixed_attention(const void* q_dec, const void* k_new, const 
   // the decode kernel's own residency would not all fit beside the prefill
   // items (measured slower), and the list keeps the longest items first.
   dp.balanced = false;
+  dp.shared_head = false;  // one workgroup per work item here (max_splits == 1 runs the per-head-group form)
   const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
   return dtype == MSGL_BF16 ? mixed_dim<bf16_t>(pp, dp, num_decode, max_extend_len, head_dim, group, s)

@@ -67,9 +67,14 @@ using namespace dec;
 // Occupancy floor: 16-bit queries with D <= 128 and up to 2 query heads per kv
 // head fit 3 wavefronts per SIMD (168 VGPRs) without spilling, which keeps
 // more K/V loads in flight per CU; the rest keep MSGL_DECODE_MIN_WAVES.
+#ifndef MSGL_DECODE_G2_MIN_WAVES
+#define MSGL_DECODE_G2_MIN_WAVES 3
+#endif
 template <typename T, int D, int G>
 constexpr int decode_min_waves() {
-  return (sizeof(T) == 2 && D <= 128 && G <= 2 && MSGL_DECODE_MIN_WAVES < 3) ? 3 : MSGL_DECODE_MIN_WAVES;
+  return (sizeof(T) == 2 && D <= 128 && G <= 2 && MSGL_DECODE_MIN_WAVES < MSGL_DECODE_G2_MIN_WAVES)
+             ? MSGL_DECODE_G2_MIN_WAVES
+             : MSGL_DECODE_MIN_WAVES;
 }
 
 // Instantiations with the key-range form built in: the shapes where its chunk
@@ -85,6 +90,14 @@ template <typename T, typename KV, int D, int G>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_min_waves<T, D, G>())))
 void paged_decode_kernel(DecodeParams p) {
   paged_decode_body<T, KV, D, G, decode_ranges<T, KV, D, G>()>(p, blockIdx.x);
+}
+
+// The shared-head form (max_splits == 1): kSharedWaves wavefronts per
+// (request, kv head), no merge.
+template <typename T, typename KV, int D, int G>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(decode_min_waves<T, D, G>())))
+void paged_decode_shared_kernel(DecodeParams p) {
+  if constexpr (decode_shared<T, KV, D, G>()) paged_decode_body<T, KV, D, G, false, true>(p, blockIdx.x);
 }
 
 template <typename T, int D, int G>
@@ -231,12 +244,31 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeP
 }
 
 template <typename T, typename KV, int D, int G>
-static int launch_decode(const DecodeParams& p, int batch, hipStream_t stream) {
+static int launch_decode(const DecodeParams& p_in, int batch, hipStream_t stream) {
+  DecodeParams p = p_in;
   const int nwaves = p.hkv < MSGL_DECODE_WAVES_PER_WG ? p.hkv : MSGL_DECODE_WAVES_PER_WG;
   const size_t lds = decode_lds_bytes<KV, D>(nwaves);
   if (!p.planned) {
     hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
     MSGL_CHECK_LAUNCH("msgl_paged_decode (plan)");
+  }
+  if constexpr (decode_shared<T, KV, D, G>()) {
+    if (p.shared_head) {  // one launch, no merge: kSharedWaves wavefronts per (request, kv head)
+      if (std::is_same<KV, fp8e4m3>::value && p.k_new != nullptr) {
+        // fp8 pools: the quantising store first (the waves of a workgroup do not
+        // read back a slot another of them wrote), then the decode reads it
+        const int st = msgl_store_kv_fp8(p.k_new, p.v_new, p.out_loc, p.k_pool_w, p.v_pool_w, p.kv_scale_w, batch,
+                                         p.hkv, D, p.num_slots, std::is_same<T, bf16_t>::value ? MSGL_BF16 : MSGL_F16,
+                                         stream);
+        if (st != MSGL_OK) return st;
+        p.k_new = p.v_new = nullptr;
+        p.out_loc = nullptr;
+      }
+      launch_main(paged_decode_shared_kernel<T, KV, D, G>, dim3((unsigned)(dec::decode_items(p) * p.hpg)),
+                  dim3(64 * kSharedWaves), decode_shared_lds_bytes<KV, D, G>(), stream, p);
+      MSGL_CHECK_LAUNCH("msgl_paged_decode");
+      return MSGL_OK;
+    }
   }
   launch_main(paged_decode_kernel<T, KV, D, G>, dim3((unsigned)dec::decode_items(p)), dim3(64 * nwaves), lds, stream,
               p);
@@ -259,6 +291,16 @@ struct MergeLaunch {
     const int units = batch * p.hkv;
     launch_main(paged_decode_merge_kernel<T, D, G>, dim3((units + 3) / 4), dim3(256), 0, stream, p, batch);
     MSGL_CHECK_LAUNCH("msgl_paged_decode_merge");
+    return MSGL_OK;
+  }
+};
+
+// Whether the instantiation has the shared-head form (max_splits == 1).
+struct SharedOK {
+  bool* out;
+  template <typename T, typename KV, int D, int G>
+  int run() const {
+    *out = decode_shared<T, KV, D, G>();
     return MSGL_OK;
   }
 };
@@ -664,6 +706,14 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
   p.balanced = false;
   p.skip_merge = false;
   p.nranges = 1;
+  p.shared_head = false;
+  p.hpg = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
+  if (max_splits == 1) {
+    bool shared = false;
+    const int st = dispatch(SharedOK{&shared}, dtype, kv_scale != nullptr, head_dim, num_qo_heads / num_kv_heads, fn);
+    if (st != MSGL_OK) return st;
+    p.shared_head = shared;
+  }
   if (max_splits > 1) {
     const int nwaves = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
     int resident = 0;

@@ -150,9 +150,13 @@ class HipAttnBackend(BaseAttnBackend):
             ops.validate_metadata(kv_indptr, kv_indices, None, num_slots=self.kv_cache.num_tokens,
                                   q_indptr=q_indptr, num_tokens=num_tokens)
 
-    def _decode_meta(self, kv_indptr, kv_indices, b: int, max_len: int) -> HipDecodeMetadata:
+    def _decode_meta(self, kv_indptr, kv_indices, lens: np.ndarray) -> HipDecodeMetadata:
         cfg = self.config
-        splits = ops.default_splits(b, cfg.num_kv_heads, max_len)
+        b, max_len = len(lens), int(lens.max())
+        if getattr(self.kv_cache, "quantized", False):
+            splits = ops.default_splits(b, cfg.num_kv_heads, max_len)
+        else:  # near-uniform batches that fill the device: one launch, no merge
+            splits = ops.decode_splits_for(lens, cfg.num_kv_heads)
         # a workspace per step, so a step prepared while the previous one still
         # runs (scheduler/scheduler.py:88-118) never touches the running step's plan
         ws = torch.empty(ops.decode_workspace_bytes(b, cfg.num_qo_heads, cfg.num_kv_heads, cfg.head_dim, splits),
@@ -188,7 +192,7 @@ class HipAttnBackend(BaseAttnBackend):
         reqs = batch.reqs
         idx = self._step_indices(reqs, np.zeros(len(reqs), dtype=bool))
         self._validate(idx["kv_indptr"], idx["kv_indices"])
-        return self._decode_meta(idx["kv_indptr"], idx["kv_indices"], len(reqs), idx["max_len"])
+        return self._decode_meta(idx["kv_indptr"], idx["kv_indices"], np.array([r.device_len for r in reqs]))
 
     def _pending_store(self, layer_id: int, num_rows: int):
         """The layer's deferred store, or None (stored now if it is not one row per decode request)."""
@@ -268,8 +272,7 @@ class HipAttnBackend(BaseAttnBackend):
         t = idx["num_tokens"]
         self._validate(idx["kv_indptr"], idx["kv_indices"], idx["q_indptr"], t)
         lens = np.array([r.device_len for r in reqs])
-        dec = self._decode_meta(idx["kv_indptr"][: nd + 1], idx["kv_indices"], nd,
-                                int(lens[:nd].max()) if nd else 1) if nd else None
+        dec = self._decode_meta(idx["kv_indptr"][: nd + 1], idx["kv_indices"], lens[:nd]) if nd else None
         pf = None
         if nd < len(reqs):
             pf = self._prefill_device(idx["q_indptr"][nd:], idx["kv_indptr"][nd:], idx["kv_indices"],

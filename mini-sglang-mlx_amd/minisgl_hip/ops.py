@@ -116,6 +116,31 @@ def default_splits(batch: int, num_kv_heads: int, max_seq_len: int = 0) -> int:
     return int(_lib.load().msgl_paged_decode_default_splits(batch, num_kv_heads, max_seq_len))
 
 
+# Resident 4-wavefront decode workgroups of MI355X (256 CUs x 3 at the decode
+# kernel's register budget): a shared-head launch needs this many (request, kv
+# head) pairs to fill the device.
+SHARED_HEAD_MIN_UNITS = 768
+
+
+def decode_splits_for(lens, num_kv_heads: int) -> int:
+    """max_splits for a decode batch whose lengths the caller knows (host array).
+
+    1 -- the shared-head form: the four wavefronts of a workgroup split one
+    (request, kv head)'s keys and combine in LDS, one launch and no merge --
+    when the pairs fill the device, no wavefront gets more than 512 keys and the
+    lengths are near-uniform (longest <= 1.25 x mean: a ragged batch leaves
+    wavefronts of short requests idle while long ones run, where the split form
+    balances chunks of <= 512 keys). Otherwise the library default."""
+    import numpy as np
+
+    lens = np.asarray(lens, dtype=np.int64)
+    b = len(lens)
+    mx = int(lens.max()) if b else 0
+    if (b * num_kv_heads >= SHARED_HEAD_MIN_UNITS and 0 < mx <= 2048 and mx <= 1.25 * float(lens.mean())):
+        return 1
+    return default_splits(b, num_kv_heads, mx)
+
+
 def decode_workspace_bytes(batch: int, num_qo_heads: int, num_kv_heads: int, head_dim: int, max_splits: int) -> int:
     return int(
         _lib.load().msgl_paged_decode_workspace_size(batch, num_qo_heads, num_kv_heads, head_dim, max_splits)

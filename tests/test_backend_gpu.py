@@ -233,3 +233,47 @@ def test_backend_validation_rejects_slots_outside_the_pool(cuda_device):
     backend._mirrored[:] = 0  # send the rows again
     with pytest.raises(ValueError, match="outside the pool"):
         backend.prepare_metadata(Batch(reqs=reqs, phase="decode"))
+
+
+def test_uniform_decode_batch_runs_shared_head_form(cuda_device):
+    """100 requests of near-uniform length (enough (request, kv head) pairs to fill
+    the device): the backend picks max_splits = 1 (four wavefronts per
+    (request, kv head), combined in LDS, no merge launch); sampled requests vs
+    the oracle, and the fused store lands at out_loc."""
+    dt = torch.bfloat16
+    cfg = ModelConfig(num_qo_heads=16, num_kv_heads=8, head_dim=128, num_layers=2)
+    kv = MHAKVCache(2, 65536, 8, 128, dt, cuda_device)
+    table = np.zeros((100, 512), dtype=np.int32)
+    backend = create_attention_backend("hip", cfg, kv, table)
+    rng = np.random.default_rng(8)
+    free = rng.permutation(65536).astype(np.int32)
+    hist = rng.integers(400, 450, size=100)
+    reqs = [Req(input_ids=np.zeros(n + 1, np.int32), table_idx=i, cached_len=int(n)) for i, n in enumerate(hist)]
+    free = oracle.allocate_paged(table, free, list(range(100)), [0] * 100, [int(n) for n in hist], 1)
+    free = oracle.allocate_paged(table, free, list(range(100)), [r.cached_len for r in reqs],
+                                 [r.device_len for r in reqs], 1)
+    for layer in range(2):
+        kv.k[layer].copy_(randn(kv.k[layer].shape, 130 + layer, dt).to(cuda_device))
+        kv.v[layer].copy_(randn(kv.v[layer].shape, 140 + layer, dt).to(cuda_device))
+    rows = [r.table_idx for r in reqs]
+    device = [r.device_len for r in reqs]
+    pos, out_loc = oracle.prepare_batch_indices(table, rows, [r.cached_len for r in reqs], device)
+    batch = Batch(reqs=reqs, phase="decode")
+    batch.out_loc = i32(out_loc, cuda_device)
+    backend.prepare_metadata(batch)
+    assert batch.attn_metadata.max_splits == 1
+    pick = [0, 1, 50, 98, 99]
+    for layer in range(2):
+        q = randn((100, 16, 128), 150 + layer, dt).to(cuda_device)
+        k = randn((100, 8, 128), 160 + layer, dt).to(cuda_device)
+        v = randn((100, 8, 128), 170 + layer, dt).to(cuda_device)
+        print(f"case backend shared-head layer={layer}", flush=True)
+        kv.store_kv(k, v, batch.out_loc, layer)
+        o = backend.forward(q, k, v, layer, batch)
+        torch.cuda.synchronize()
+        loc = batch.out_loc.long()
+        assert torch.equal(kv.k_cache(layer)[loc], k) and torch.equal(kv.v_cache(layer)[loc], v)
+        kvi, mask = oracle.naive_decode_metadata(table, [rows[i] for i in pick], [device[i] for i in pick])
+        ref = oracle.naive_forward_decode(to_np64(q[pick]), to_np64(kv.k[layer]), to_np64(kv.v[layer]), kvi, mask,
+                                          128**-0.5)
+        assert_close(o[pick], ref, dt, f"shared-head layer {layer}")

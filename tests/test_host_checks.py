@@ -62,3 +62,15 @@ def test_scale_value_reads_cpu_tensors_and_floats():
     assert ops.scale_value(torch.tensor([0.125])) == 0.125
     with pytest.raises(ValueError):
         ops.scale_value(torch.zeros(2))
+
+
+def test_decode_split_choice_for_known_lengths():
+    rng = np.random.default_rng(0)
+    # near-uniform batch filling the device: the shared-head form (one launch, no merge)
+    assert ops.decode_splits_for(np.full(128, 1144), 8) == 1
+    assert ops.decode_splits_for(rng.integers(1000, 1200, size=96), 8) == 1
+    # ragged lengths, too few (request, kv head) pairs, or more than 512 keys per wavefront: the split forms
+    ragged = rng.integers(200, 2049, size=128)
+    assert ops.decode_splits_for(ragged, 8) == ops.default_splits(128, 8, int(ragged.max()))
+    assert ops.decode_splits_for(np.full(95, 1144), 8) != 1
+    assert ops.decode_splits_for(np.full(128, 3000), 8) != 1
