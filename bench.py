@@ -404,7 +404,7 @@ def bench_decode_fp8(args, dev):
                                        new_kv=(ks[layer], vs[layer], out_loc), merge=False)
             if ev and layer == timed and splits > 1:
                 ops.profile_next_launch(ev[2], ev[3])
-            ops.paged_decode_merge(outs[layer], indptr, None, HKV, splits, ws)
+            ops.paged_decode_merge(outs[layer], indptr, None, HKV, splits, ws, kv_fp8=True)
 
     sec, kern_s, merge_s = _timed(args, run, nev=4)
     if splits == 1:

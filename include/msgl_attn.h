@@ -223,12 +223,13 @@ int msgl_paged_decode_planned_ex(const void* q, const void* k_new, const void* v
  * out[b] = sum_s 2^(m_s - M) acc_s / sum_s 2^(m_s - M) l_s over the chunks of
  * every request cut into more than one (the combine of the Metal kernel's
  * simdgroup merge, attention/metal.py:75-94). Same indices, sizes, dtype,
- * max_splits and workspace as the decode call; nothing to do when
- * max_splits == 1.
+ * max_splits and workspace as the decode call, and kv_fp8 = 1 when that call
+ * ran over fp8 pools (its split form depends on the kernel it ran); nothing to
+ * do when max_splits == 1.
  */
 int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* seq_lens, int32_t batch, int32_t num_qo_heads,
-                            int32_t num_kv_heads, int32_t head_dim, int32_t dtype, int32_t max_splits, void* out,
-                            void* workspace, int64_t workspace_bytes, void* stream);
+                            int32_t num_kv_heads, int32_t head_dim, int32_t dtype, int32_t kv_fp8, int32_t max_splits,
+                            void* out, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
  * Ragged chunked-prefill attention over a paged pool, one launch per batch.

@@ -140,8 +140,7 @@ struct DecodeParams {
   // work list (plan kernel output, in the workspace)
   int* meta;        // [0] items in the plan, [1] batch-wide chunk length, [2] the plan's max_splits
                     // (with key offsets), [3] max_b L_b, [4..6] the batch, max_splits and kv-head
-                    // groups the plan was built for, [7] the key ranges the last decode launch
-                    // over this plan split by (0: per-request chunks), read by the merge
+                    // groups the plan was built for
   int4* plan;       // (request, split, kv-head group, 0), longest first
   int64_t* tok_off; // balanced split: [B+1] tokens of the requests before b (tok_off[B] = all)
   int nranges;      // balanced split: key ranges of the launch (grid / ngrp)
@@ -600,9 +599,6 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
     }
   }
   const bool bal = RANGES && balanced_launch(p);
-  // the form this launch splits by, for the merge (which need not know the
-  // kernel's residency or whether key ranges were built in)
-  if (wg == 0 && threadIdx.x == 0 && plan_matches(p)) p.meta[7] = bal ? p.nranges : 0;
   int b, kgrp, start = 0, L = 0, t0 = 0, t1 = 0, split = 0, n = 1;
   int64_t k = 0, rl = 1, g0 = 0, g1 = 0;
   if (bal) {
@@ -680,15 +676,14 @@ __device__ __forceinline__ void paged_decode_merge_body(const DecodeParams& p, i
   const int b = unit / p.hkv, kvh = unit % p.hkv;
   if (!plan_matches(p)) return;
   int n, chunk;
-  const int nranges = p.meta[7];  // the key ranges the decode launch split by (0: per-request chunks)
-  if (nranges > 0) {  // the ranges request b overlaps; no key: the defined zero output
+  if (balanced_launch(p)) {  // the ranges request b overlaps; no key: the defined zero output
     const int64_t ob = p.tok_off[b], ob1 = p.tok_off[b + 1];
     if (ob1 == ob) {
       T* o = reinterpret_cast<T*>(p.out) + ((int64_t)b * p.hq + kvh * G) * D;
       for (int i = lane; i < G * D; i += 64) o[i] = from_f32<T>(0.f);
       return;
     }
-    const int64_t rl = balanced_range(p.tok_off[p.batch], p.meta[3], nranges, p.max_splits);
+    const int64_t rl = balanced_range(p.tok_off[p.batch], p.meta[3], p.nranges, p.max_splits);
     n = (int)((ob1 - 1) / rl - ob / rl + 1);
   } else {
     const int L = p.seq_lens ? p.seq_lens[b] : p.kv_indptr[b + 1] - p.kv_indptr[b];

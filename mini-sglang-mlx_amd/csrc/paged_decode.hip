@@ -771,8 +771,8 @@ extern "C" int msgl_paged_decode_planned_ex(const void* q, const void* k_new, co
 
 extern "C" int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* seq_lens, int32_t batch,
                                        int32_t num_qo_heads, int32_t num_kv_heads, int32_t head_dim, int32_t dtype,
-                                       int32_t max_splits, void* out, void* workspace, int64_t workspace_bytes,
-                                       void* stream) {
+                                       int32_t kv_fp8, int32_t max_splits, void* out, void* workspace,
+                                       int64_t workspace_bytes, void* stream) {
   using namespace msgl;
   clear_error();
   MSGL_CHECK_ARG(batch >= 0 && batch <= 65535, "msgl_paged_decode_merge: batch must be in [0, 65535]");
@@ -810,6 +810,16 @@ extern "C" int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* 
   p.hkv = num_kv_heads;
   p.max_splits = max_splits;
   p.ngrp = decode_groups(num_kv_heads);
+  // the split form the decode launch chose: key ranges are sized by that
+  // kernel's residency, so it is derived the way the decode call derives it
+  const int nwaves = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
+  int resident = 0;
+  bool ranges = false;
+  const int st = dispatch(Resident{nwaves, &resident, &ranges}, dtype, kv_fp8 != 0, head_dim,
+                          num_qo_heads / num_kv_heads, "msgl_paged_decode_merge");
+  if (st != MSGL_OK) return st;
+  p.balanced = ranges;
+  p.nranges = std::max(1, resident * MSGL_DECODE_RANGE_ROUNDS / p.ngrp);
   return dispatch(MergeLaunch{p, batch, (hipStream_t)stream}, dtype, false, head_dim, num_qo_heads / num_kv_heads,
                   "msgl_paged_decode_merge");
 }

@@ -147,7 +147,7 @@ SIGNATURES["msgl_paged_decode_planned_ex"] = (
 )
 SIGNATURES["msgl_paged_decode_merge"] = (
     ctypes.c_int,
-    [_c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_i64, _c_p],
+    [_c_p, _c_p, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_i32, _c_p, _c_p, _c_i64, _c_p],
 )
 MSGL_DECODE_NO_MERGE = 1
 

@@ -363,10 +363,12 @@ def paged_decode_merge(
     num_kv_heads: int,
     max_splits: int,
     workspace: torch.Tensor,
+    kv_fp8: bool = False,
 ) -> torch.Tensor:
     """The split-K merge of a ``paged_decode_attention(..., planned=True,
-    merge=False)`` call with the same indices, sizes and workspace: completes
-    ``out`` [B, Hq, D] in place (msgl_paged_decode_merge)."""
+    merge=False)`` call with the same indices, sizes and workspace (``kv_fp8``:
+    that call ran over fp8 pools): completes ``out`` [B, Hq, D] in place
+    (msgl_paged_decode_merge)."""
     b, hq, d = out.shape
     dev = out.device
     _check_device("out", out, dev)
@@ -375,8 +377,9 @@ def paged_decode_merge(
     if getattr(workspace, "_msgl_decode_plan", None) != (b, num_kv_heads, max_splits):
         raise ValueError("paged_decode_merge: the workspace holds no plan for these sizes")
     status = _lib.load().msgl_paged_decode_merge(
-        _lib.ptr(kv_indptr), _lib.ptr(seq_lens), b, hq, num_kv_heads, d, _lib.dtype_code(out.dtype), int(max_splits),
-        _lib.ptr(out), _lib.ptr(workspace), workspace.numel() * workspace.element_size(), _lib.current_stream(dev),
+        _lib.ptr(kv_indptr), _lib.ptr(seq_lens), b, hq, num_kv_heads, d, _lib.dtype_code(out.dtype), int(kv_fp8),
+        int(max_splits), _lib.ptr(out), _lib.ptr(workspace), workspace.numel() * workspace.element_size(),
+        _lib.current_stream(dev),
     )
     _lib.check(status, "msgl_paged_decode_merge")
     return out

@@ -126,7 +126,7 @@ def test_split_decode_launch_equals_one_call(cuda_device):
     o = torch.empty_like(q)
     ops.paged_decode_attention(q, kq2, vq2, ip, ix, d**-0.5, max_splits=6, workspace=ws, out=o,
                                new_kv=(kn, vn, loc), planned=True, kv_scale=sc2, merge=False)
-    ops.paged_decode_merge(o, ip, None, hkv, 6, ws)
+    ops.paged_decode_merge(o, ip, None, hkv, 6, ws, kv_fp8=True)
     torch.cuda.synchronize()
     assert torch.equal(a, o), "split fp8 launch differs"
     assert torch.equal(sc, sc2) and torch.equal(kq.view(torch.uint8), kq2.view(torch.uint8))
