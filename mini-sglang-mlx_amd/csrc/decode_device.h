@@ -193,10 +193,12 @@ template <typename KV, int D>
 constexpr int k_lds_stride() { return D * (int)sizeof(KV) + 16; }
 
 // Dynamic LDS floats of a decode workgroup of nwaves wavefronts: the staged
-// slots, then per wave the P/alpha/(m, l) tiles and the K re-layout tile.
+// slots, then per wave the P/alpha/(m, l) tiles and the K re-layout tile, then
+// (fp8 pools) the staged tokens' (K, V) scales of the workgroup's kv heads.
 template <typename KV, int D>
 __host__ __device__ constexpr int decode_lds_floats(int nwaves) {
-  return kSeg + kSlotPad + nwaves * (kLdsPerWave + 16 * k_lds_stride<KV, D>() / 4);
+  return kSeg + kSlotPad + nwaves * (kLdsPerWave + 16 * k_lds_stride<KV, D>() / 4) +
+         (std::is_same<KV, fp8e4m3>::value ? (kSeg + kSlotPad) * nwaves * 2 : 0);
 }
 
 // Minimum wavefronts per SIMD the register allocator must allow (occupancy).
@@ -263,6 +265,8 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
   const int nwaves = blockDim.x >> 6;
   constexpr int KRS = k_lds_stride<KV, D>();
   float* lds = lds_all + kSeg + kSlotPad + wave * (kLdsPerWave + 16 * KRS / 4);
+  // fp8 pools, split form: [staged token][workgroup head][K, V] scales
+  float* scale_lds = lds_all + kSeg + kSlotPad + nwaves * (kLdsPerWave + 16 * KRS / 4);
   float* P_lds = lds;              // [16][16]
   float* A_lds = lds + 256;        // [16]
   float* ML_lds = lds + 256 + 16;  // [16][2]
@@ -377,7 +381,35 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
         slots_lds[i] = slot_of(p.kv_indices, nidx, start, tok, p.page_size, p.num_slots);
       }
       __syncthreads();
-      if (!active) continue;
+      // fp8 pools, split form: the (K, V) scales of the workgroup's kv heads for
+      // every staged token, one 4-byte LDS DMA per lane -- each token's scale
+      // line is requested once per workgroup instead of once per wavefront (the
+      // heads of a slot are neighbours, [slot][head][K, V]). The transfers land
+      // while the first tiles load; the waves wait for them (and meet at a
+      // barrier) just before their first compute of the segment.
+      constexpr bool SCL = Q8 && !SHARED;
+      if constexpr (SCL) {
+        const int nd = 2 * nwaves;  // dwords per token
+        const int total = (ntile + NST - 1) * 16 * nd;
+        const int h0 = kgrp * nwaves;
+        const uint32_t sbase = (uint32_t)(uintptr_t)((MSGL_LDS float*)scale_lds);
+        for (int c = wave; c * 64 < total; c += nwaves) {
+          const int idx = c * 64 + lane;
+          if (idx < total) {
+            const int t = idx / nd, d = idx - t * nd;
+            const int h = min(h0 + (d >> 1), p.hkv - 1);  // heads past hkv: an inactive wave's, never read
+            dma4(p.kv_scale + ((int64_t)slots_lds[t] * p.hkv + h) * 2 + (d & 1),
+                 __builtin_amdgcn_readfirstlane(sbase + c * 256));
+          }
+        }
+      }
+      if (!active) {
+        if constexpr (SCL) {  // this wave's transfers landed; meet the others' first-compute barrier
+          vm_wait<0>();
+          __syncthreads();
+        }
+        continue;
+      }
 
       // Prefetches past the segment end read the padded slot list (the last
       // valid slot, one row per tile, already fetched): every path through the
@@ -393,7 +425,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
           buf.k[i] = ld16_stream(is_new ? knew_p : kbase_p + off);
           buf.v[i] = ld16_stream(is_new ? vnew_p : vbase_p + off);
         }
-        if (Q8) {  // the K and V scales of the token in this lane's MFMA column: one 8-byte load
+        if (Q8 && !SCL) {  // the K and V scales of the token in this lane's MFMA column: one 8-byte load
           const float2 sc = reinterpret_cast<const float2*>(p.kv_scale)[(int64_t)slots_lds[base + r] * p.hkv + kvh_c];
           buf.ks = sc.x;
           buf.vs = sc.y;
@@ -419,7 +451,13 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
           }
         }
         // online softmax (exp2 domain); a quantised row's scale multiplies its scores
-        const float sc = Q8 ? p.scale_log2 * buf.ks : p.scale_log2;
+        float ks = buf.ks, vs = buf.vs;
+        if constexpr (SCL) {
+          const float2 kv = *reinterpret_cast<const float2*>(scale_lds + ((tile * 16 + r) * nwaves + wave) * 2);
+          ks = kv.x;
+          vs = kv.y;
+        }
+        const float sc = Q8 ? p.scale_log2 * ks : p.scale_log2;
         const bool valid = tile * 16 + r < seg_len;
         float pr[4] = {0.f, 0.f, 0.f, 0.f}, al[4] = {1.f, 1.f, 1.f, 1.f};
 #pragma unroll
@@ -434,7 +472,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
         }
         wave_lds_sync();  // previous tile's LDS reads are done
         // P V weights; a quantised V row's scale is folded into its weight (l keeps the plain weights)
-        const float vsc = Q8 ? buf.vs : 1.f;
+        const float vsc = Q8 ? vs : 1.f;
         *reinterpret_cast<f32x4*>(P_lds + r * 16 + 4 * g4) = f32x4{pr[0] * vsc, pr[1] * vsc, pr[2] * vsc, pr[3] * vsc};
         if (r == 0) *reinterpret_cast<f32x4*>(A_lds + 4 * g4) = f32x4{al[0], al[1], al[2], al[3]};
         wave_lds_sync();
@@ -473,6 +511,12 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
           const int j = j0 + k;
           if (j >= nloc) break;
           issue(buf[(k + NST - 1) % NST], tile0 + (j + NST - 1) * TS);
+          if constexpr (SCL) {
+            if (j == 0) {  // the scale transfers, issued before every row load, and tile 0 have landed
+              vm_wait<(NST - 1) * 2 * NLV>();
+              __syncthreads();
+            }
+          }
           compute(buf[k], tile0 + j * TS);
         }
       }

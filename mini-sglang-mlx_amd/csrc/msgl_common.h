@@ -243,6 +243,66 @@ __device__ __forceinline__ float fp8_quantize_chunk(const u32x4& in, int lpr, ui
   return amax;
 }
 
+#define MSGL_LDS __attribute__((address_space(3)))
+
+// LDS DMA (global_load_lds_dword{,x4}): `bytes` per lane from global memory
+// into LDS at lds_addr + bytes * lane (lds_addr wave-uniform, in m0). The
+// caller waits for the transfer with vm_wait and makes it visible to the
+// other wavefronts with a barrier.
+//
+// Issued as inline assembly: with __builtin_amdgcn_global_load_lds the
+// compiler cannot tell which LDS bytes a transfer in flight writes (it has no
+// alias scopes for them), so it drains every transfer (vmcnt(0)) before each
+// LDS read of a ring, which serialises a pipeline over one. The statement is
+// self-contained: it saves m0, sets it, waits the one wait state an SALU write
+// of m0 needs before an LDS DMA reads it (GFX9 family), issues the transfer
+// and restores m0, so whatever the compiler keeps in m0 survives it.
+// MSGL_DMA_BUILTIN=1 builds the builtin form instead.
+#ifndef MSGL_DMA_BUILTIN
+#define MSGL_DMA_BUILTIN 0
+#endif
+__device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
+#if MSGL_DMA_BUILTIN
+  __builtin_amdgcn_global_load_lds(g, (MSGL_LDS void*)(uintptr_t)lds_addr, 16, 0, 0);
+#else
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dwordx4 %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds_addr)
+      : "memory");
+#endif
+}
+
+// 4 bytes per active lane (see dma16).
+__device__ __forceinline__ void dma4(const void* g, uint32_t lds_addr) {
+#if MSGL_DMA_BUILTIN
+  __builtin_amdgcn_global_load_lds(g, (MSGL_LDS void*)(uintptr_t)lds_addr, 4, 0, 0);
+#else
+  uint32_t saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %2\n\t"
+      "s_nop 0\n\t"
+      "global_load_lds_dword %1, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "v"(g), "s"(lds_addr)
+      : "memory");
+#endif
+}
+
+// Wait until at most N vector memory operations of this wavefront are in
+// flight (they complete in issue order).
+template <int N>
+__device__ __forceinline__ void vm_wait() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
 // Ordering point for LDS traffic between lanes of one wavefront.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");

@@ -95,7 +95,6 @@ __device__ __forceinline__ void chunk_geometry(int kv_end, int splits, int chunk
   n = min(splits, (kv_end + clen - 1) / clen);
 }
 
-#define MSGL_LDS __attribute__((address_space(3)))
 typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
 typedef __fp16 f16x4_t __attribute__((__vector_size__(4 * sizeof(__fp16))));
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -119,39 +118,6 @@ __device__ __forceinline__ uint2 lds_read_tr16<f16_t>(const uint8_t* p) {
   return __builtin_bit_cast(uint2, __builtin_amdgcn_ds_read_tr16_b64_v4f16(lp));
 }
 
-// LDS DMA (global_load_lds_dword{,x4}): `bytes` per lane from global memory
-// into LDS at lds_addr + bytes * lane (lds_addr wave-uniform, in m0). The
-// caller waits for the transfer with vm_wait and makes it visible to the
-// other wavefronts with a barrier.
-//
-// Issued as inline assembly: with __builtin_amdgcn_global_load_lds the
-// compiler cannot tell which LDS bytes a transfer in flight writes (it has no
-// alias scopes for them), so it drains every transfer (vmcnt(0)) before each
-// LDS read of the ring, which serialises the pipeline below. The statement is
-// self-contained: it saves m0, sets it, waits the one wait state an SALU write
-// of m0 needs before an LDS DMA reads it (GFX9 family), issues the transfer
-// and restores m0, so whatever the compiler keeps in m0 survives it.
-// MSGL_PREFILL_DMA_BUILTIN=1 builds the builtin form instead.
-#ifndef MSGL_PREFILL_DMA_BUILTIN
-#define MSGL_PREFILL_DMA_BUILTIN 0
-#endif
-__device__ __forceinline__ void dma16(const void* g, uint32_t lds_addr) {
-#if MSGL_PREFILL_DMA_BUILTIN
-  __builtin_amdgcn_global_load_lds(g, (MSGL_LDS void*)(uintptr_t)lds_addr, 16, 0, 0);
-#else
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dwordx4 %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(g), "s"(lds_addr)
-      : "memory");
-#endif
-}
-
 // The value of lane l ^ 32 combined with this lane's, on the VALU:
 // v_permlane32_swap of x with itself leaves (x[l % 32], x[l % 32 + 32]) in
 // every lane (checked on gfx950), so max / sum of the pair needs no LDS
@@ -167,24 +133,6 @@ __device__ __forceinline__ float xor32_max(float x) {
 __device__ __forceinline__ float xor32_sum(float x) {
   const f32x2_t h = halves(x);
   return h[0] + h[1];
-}
-
-// 4 bytes per active lane (see dma16).
-__device__ __forceinline__ void dma4(const void* g, uint32_t lds_addr) {
-#if MSGL_PREFILL_DMA_BUILTIN
-  __builtin_amdgcn_global_load_lds(g, (MSGL_LDS void*)(uintptr_t)lds_addr, 4, 0, 0);
-#else
-  uint32_t saved;
-  asm volatile(
-      "s_mov_b32 %0, m0\n\t"
-      "s_mov_b32 m0, %2\n\t"
-      "s_nop 0\n\t"
-      "global_load_lds_dword %1, off\n\t"
-      "s_mov_b32 m0, %0"
-      : "=&s"(saved)
-      : "v"(g), "s"(lds_addr)
-      : "memory");
-#endif
 }
 
 // ds_read_b64_tr_b8: within each 16-lane group, lane i receives byte i%8 of
@@ -213,11 +161,6 @@ __device__ __forceinline__ u32x4 fp8x8<f16_t>(uint32_t w0, uint32_t w1) {
                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w0, 1.0f, true)),
                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, false)),
                __builtin_bit_cast(uint32_t, __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w1, 1.0f, true))};
-}
-
-template <int N>
-__device__ __forceinline__ void vm_wait() {
-  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
 typedef float f32x16 __attribute__((ext_vector_type(16)));
