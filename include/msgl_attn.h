@@ -302,8 +302,12 @@ int msgl_prefill_ragged_planned(const void* q, const void* k_pool, const void* v
  *                                      [0, device_len)); with page_size > 1 page
  *                                      ids of ceil(device_len / page_size) pages
  * T = q_indptr[R] and kv_indptr[R] are left on the device; outputs stop at
- * token_capacity / kv_capacity. positions, out_loc and last_indices may be
- * NULL. Table entries outside the table read as -1. Two launches.
+ * token_capacity / kv_capacity, and the offsets written (q_indptr, kv_indptr,
+ * last_indices) are clamped to those capacities, so a launch that reads them
+ * next stays inside the outputs (undersized capacities give truncated, not
+ * out-of-bounds, metadata; size them from the host-known lengths).
+ * positions, out_loc and last_indices may be NULL. Table entries outside the
+ * table read as -1. Two launches.
  */
 int msgl_build_step_indices(const int32_t* req_to_token, int64_t num_rows, int64_t row_stride,
                             const int32_t* table_idx, const int32_t* cached_len, const int32_t* device_len,

@@ -233,6 +233,23 @@ constexpr bool decode_shared() {
          (decode_lds_floats<KV, D>(kSharedWaves) + kSharedWaves * (G * D + 2 * G)) * 4 <= 65536;
 }
 
+// Workgroup order of a launch whose items are ngrp consecutive kv-head groups
+// (n workgroups, a multiple of ngrp): the command processor hands workgroups
+// to the 8 XCDs of MI355X round-robin, so item i's groups are given ids that
+// differ by 8 inside a block of 8*ngrp workgroups (the last block: its m
+// items' groups m apart) and run on one XCD at about the same time. Over fp8
+// pools a token's 128-byte scale line (all kv heads of the slot) is then
+// fetched from HBM once and hit in that XCD's L2 by the other groups.
+#ifndef MSGL_DECODE_FP8_XCD_GROUPS
+#define MSGL_DECODE_FP8_XCD_GROUPS 1
+#endif
+__device__ __forceinline__ int xcd_group_order(int wg, int n, int ngrp) {
+  const int blk = 8 * ngrp;
+  const int kb = wg / blk, j = wg - kb * blk;
+  const int m = max(1, min(8, (n - kb * blk) / ngrp));  // items in this block
+  return (kb * 8 + j % m) * ngrp + j / m;
+}
+
 // T: the query/output type; KV: the pool's storage type (T itself, or fp8e4m3
 // for a quantised pool with per-(slot, kv head) scales). RANGES: the key-range
 // form is built in (its chunk loop costs registers; without it every
@@ -643,6 +660,11 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
     }
   }
   const bool bal = RANGES && balanced_launch(p);
+  if constexpr (Q8 && MSGL_DECODE_FP8_XCD_GROUPS) {
+    // fp8 pools: the kv-head groups of one item on one XCD (see xcd_group_order)
+    const int nw = bal ? p.nranges * p.ngrp : p.meta[0];
+    if (p.ngrp > 1 && wg < nw) wg = xcd_group_order(wg, nw, p.ngrp);
+  }
   int b, kgrp, start = 0, L = 0, t0 = 0, t1 = 0, split = 0, n = 1;
   int64_t k = 0, rl = 1, g0 = 0, g1 = 0;
   if (bal) {

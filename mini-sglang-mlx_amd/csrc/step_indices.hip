@@ -103,9 +103,11 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(IndexParams p) {
     int2 tot;
     block_scan2(e, kv, lds, tot);
     if (r < p.num_reqs) {
-      p.q_indptr[r + 1] = carry_q + e;
-      p.kv_indptr[r + 1] = carry_kv + kv;
-      if (p.last_indices) p.last_indices[r] = carry_q + e - 1;
+      // offsets past a capacity are clamped to it: the outputs stop there, and
+      // no launch that reads these offsets next reads past them
+      p.q_indptr[r + 1] = (int)min((int64_t)carry_q + e, p.token_capacity);
+      p.kv_indptr[r + 1] = (int)min((int64_t)carry_kv + kv, p.kv_capacity);
+      if (p.last_indices) p.last_indices[r] = (int)min((int64_t)carry_q + e, p.token_capacity) - 1;
     }
     carry_q += tot.x;
     carry_kv += tot.y;

@@ -35,12 +35,14 @@ def _table(num_reqs, max_len, page_size, seed, num_rows=None, decode=False):
     return table, rows.astype(np.int32), cached_len.astype(np.int32), device_len.astype(np.int32)
 
 
-def _build(table, rows, cached, dlen, page_size, device, num_kv=None):
+def _build(table, rows, cached, dlen, page_size, device, num_kv=None, num_tokens=None):
     extend = np.maximum(dlen - cached, 0)
     if num_kv is None:
         num_kv = int(dlen.sum()) if page_size == 1 else int(sum(oracle.div_ceil(int(L), page_size) for L in dlen))
+    if num_tokens is None:
+        num_tokens = int(extend.sum())
     out = ops.build_step_indices(i32(table, device), i32(rows, device), i32(cached, device), i32(dlen, device),
-                                 num_tokens=int(extend.sum()), num_kv=num_kv, page_size=page_size)
+                                 num_tokens=num_tokens, num_kv=num_kv, page_size=page_size)
     torch.cuda.synchronize()
     return {k: v.cpu().numpy() for k, v in out.items()}
 
@@ -80,7 +82,8 @@ def test_step_indices_decode_batch(cuda_device):
 
 
 def test_step_indices_out_of_range_and_capacity(cuda_device):
-    """Rows outside the table read as -1; outputs stop at the given capacities."""
+    """Rows outside the table read as -1; outputs stop at the given capacities
+    and the offsets are clamped to them (a launch reading them stays inside)."""
     table, rows, cached, dlen = _table(4, 50, 1, seed=3)
     rows = rows.copy()
     rows[2] = table.shape[0] + 5
@@ -93,7 +96,14 @@ def test_step_indices_out_of_range_and_capacity(cuda_device):
     np.testing.assert_array_equal(got["kv_indices"][keep], ref[keep])
     short = _build(table, rows, cached, dlen, 1, cuda_device, num_kv=10)
     np.testing.assert_array_equal(short["kv_indices"], got["kv_indices"][:10])
-    assert short["kv_indptr"][-1] == got["kv_indptr"][-1]  # the total is still reported
+    np.testing.assert_array_equal(short["kv_indptr"], np.minimum(got["kv_indptr"], 10))
+    np.testing.assert_array_equal(short["q_indptr"], got["q_indptr"])
+    t_short = int(got["q_indptr"][-1]) - 3
+    shortq = _build(table, rows, cached, dlen, 1, cuda_device, num_tokens=t_short)
+    np.testing.assert_array_equal(shortq["q_indptr"], np.minimum(got["q_indptr"], t_short))
+    np.testing.assert_array_equal(shortq["last_indices"], np.minimum(got["q_indptr"][1:], t_short) - 1)
+    np.testing.assert_array_equal(shortq["positions"], got["positions"][:t_short])
+    np.testing.assert_array_equal(shortq["kv_indptr"], got["kv_indptr"])
 
 
 def test_table_scatter(cuda_device):
