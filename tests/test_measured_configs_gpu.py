@@ -99,3 +99,77 @@ def test_8b_heads_batch256_page16_full_size(cuda_device):
     assert_close(out[pick], np.stack(ref), dt, "8b b256 page16 sampled")
     del kp, vp
     torch.cuda.empty_cache()
+
+
+def test_fp8_decode_step_measured_config(cuda_device):
+    """The fp8 decode workload as the benchmark runs it (batch 128, contexts
+    U[200,2048] seed 0, page 1, 262144-slot fp8 pools with per-(slot, kv head)
+    scales), over 4 distinct layer pools: one plan, then per layer the decode
+    launch with the quantising store fused in and no merge, then the merge.
+    Each layer's output equals store-then-decode (msgl_store_kv_fp8, then the
+    unplanned decode) bit for bit, the codes and scales at out_loc equal the
+    store's, and sampled requests match the oracle over the dequantised pool
+    (kvcache/pool.py:47-50 + attention/naive.py:50-60)."""
+    hq, hkv, d, batch, pool, layers = 16, 8, 128, 128, 262144, 4
+    c = workloads.decode_case(batch, 200, 2048, pool, 1, seed=0)
+    dev = cuda_device
+    gen = torch.Generator(device=dev).manual_seed(5)
+    dt, f8 = torch.bfloat16, torch.float8_e4m3fn
+    indptr = torch.from_numpy(c.kv_indptr).to(dev)
+    indices = torch.from_numpy(c.kv_indices).to(dev)
+    out_loc = torch.from_numpy(c.out_loc).to(dev)
+    splits = ops.default_splits(batch, hkv, int(c.lens.max()))
+    ws = ops.decode_workspace(batch, hq, hkv, d, splits, dev)
+    scale = d**-0.5
+    pools = []
+    for layer in range(layers):
+        kp = torch.empty((pool, hkv, d), dtype=f8, device=dev)
+        vp = torch.empty_like(kp)
+        sc = torch.empty((pool, hkv, 2), dtype=torch.float32, device=dev)
+        for s0 in range(0, pool, 65536):
+            rows = torch.arange(s0, s0 + 65536, dtype=torch.int32, device=dev)
+            ops.store_kv_fp8(torch.randn((65536, hkv, d), generator=gen, device=dev, dtype=dt),
+                             torch.randn((65536, hkv, d), generator=gen, device=dev, dtype=dt), rows, kp, vp, sc)
+        pools.append((kp, vp, sc))
+    qs = [torch.randn((batch, hq, d), generator=gen, device=dev, dtype=dt) for _ in range(layers)]
+    ks = [torch.randn((batch, hkv, d), generator=gen, device=dev, dtype=dt) for _ in range(layers)]
+    vs = [torch.randn((batch, hkv, d), generator=gen, device=dev, dtype=dt) for _ in range(layers)]
+    # the reference sequence first, on copies: store, then the one-call decode
+    refs, ref_pools = [], []
+    for layer in range(layers):
+        kp, vp, sc = (x.clone() for x in pools[layer])
+        ops.store_kv_fp8(ks[layer], vs[layer], out_loc, kp, vp, sc)
+        refs.append(ops.paged_decode_attention(qs[layer], kp, vp, indptr, indices, scale, max_splits=splits,
+                                               kv_scale=sc))
+        ref_pools.append((kp, vp, sc))
+    print(f"case fp8 decode step {layers} layers splits={splits}", flush=True)
+    outs = [torch.empty_like(x) for x in qs]
+    ops.paged_decode_plan(indptr, None, batch, hq, hkv, d, splits, ws)
+    for layer in range(layers):
+        kp, vp, sc = pools[layer]
+        ops.paged_decode_attention(qs[layer], kp, vp, indptr, indices, scale, max_splits=splits, out=outs[layer],
+                                   workspace=ws, new_kv=(ks[layer], vs[layer], out_loc), planned=True,
+                                   kv_scale=sc, merge=False)
+        ops.paged_decode_merge(outs[layer], indptr, None, hkv, splits, ws, kv_fp8=True)
+    torch.cuda.synchronize()
+    loc = out_loc.long()
+    for layer in range(layers):
+        kp, vp, sc = pools[layer]
+        rk, rv, rs = ref_pools[layer]
+        assert torch.equal(outs[layer], refs[layer]), f"layer {layer}: fused planned step differs from store + decode"
+        assert torch.equal(kp[loc].view(torch.uint8), rk[loc].view(torch.uint8)), f"layer {layer}: K codes"
+        assert torch.equal(vp[loc].view(torch.uint8), rv[loc].view(torch.uint8)), f"layer {layer}: V codes"
+        assert torch.equal(sc[loc], rs[loc]), f"layer {layer}: scales"
+    pick = [0, 5, 64, 127, int(np.argmax(c.lens)), int(np.argmin(c.lens))]
+    for layer in (0, layers - 1):
+        kp, vp, sc = pools[layer]
+        ref = []
+        for b in pick:
+            slots = torch.from_numpy(c.kv_indices[c.kv_indptr[b]: c.kv_indptr[b + 1]].astype(np.int64)).to(dev)
+            kb = oracle.dequantize_fp8(kp[slots].view(torch.uint8).cpu().numpy(), sc[slots][..., 0].cpu().numpy())
+            vb = oracle.dequantize_fp8(vp[slots].view(torch.uint8).cpu().numpy(), sc[slots][..., 1].cpu().numpy())
+            ref.append(oracle.sdpa(to_np64(qs[layer][b])[:, None, :], kb.transpose(1, 0, 2), vb.transpose(1, 0, 2),
+                                   scale)[:, 0])
+        assert_close(outs[layer][pick], np.stack(ref), dt, f"fp8 step layer {layer}")
+    del pools, ref_pools
+    torch.cuda.empty_cache()
