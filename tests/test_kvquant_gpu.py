@@ -87,7 +87,8 @@ def test_store_kv_fp8_skips_slots_outside_pool(cuda_device):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256), (64, 8, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256), (64, 8, 128),
+                                      (24, 12, 128), (32, 16, 64)])
 @pytest.mark.parametrize("splits", [1, None, 8])
 def test_fp8_decode_reference_grid(cuda_device, dt, hq, hkv, d, splits):
     """tests/test_attention.py:19-39's grid (B=7, lens [1,2,17,31,32,33,700], N=4096) over fp8 pools."""
@@ -136,12 +137,14 @@ def test_fp8_planned_matches_unplanned(cuda_device):
     assert torch.equal(a, b)
 
 
-def test_fp8_key_ranges_long_contexts(cuda_device):
-    """~1M keys over fp8 pools (Qwen3-0.6B heads): enough for the decode launch to
-    split by equal key ranges. The fused quantising store gives the same bits as
-    store + decode, and the result agrees with the unsplit decode (one workgroup
-    per request and kv-head group)."""
-    b, hq, hkv, d = 160, 16, 8, 128
+@pytest.mark.parametrize("hq,hkv", [(16, 8), (24, 12)])
+def test_fp8_key_ranges_long_contexts(cuda_device, hq, hkv):
+    """~1M keys over fp8 pools (Qwen3-0.6B heads; and 12 kv heads, three kv-head
+    groups): enough for the decode launch to split by equal key ranges. The
+    fused quantising store gives the same bits as store + decode, and the
+    result agrees with the unsplit decode (one workgroup per request and
+    kv-head group)."""
+    b, d = 160, 128
     c = workloads.decode_case(b, 4096, 8192, 1 << 21, 1, seed=13)
     cus = torch.cuda.get_device_properties(cuda_device).multi_processor_count
     assert int(c.lens.sum()) >= 2048 * 3 * cus // 2, "too few keys to select key ranges"
@@ -153,7 +156,7 @@ def test_fp8_key_ranges_long_contexts(cuda_device):
     v_new = randn((b, hkv, d), 413, torch.bfloat16).to(cuda_device)
     out_loc = i32(c.out_loc, cuda_device)
     ip, ix = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
-    print("case fp8 key ranges", flush=True)
+    print(f"case fp8 key ranges hkv={hkv}", flush=True)
     ops.store_kv_fp8(k_new, v_new, out_loc, kp, vp, sc)
     a = ops.paged_decode_attention(q, kp, vp, ip, ix, d**-0.5, kv_scale=sc, max_seq_len=int(c.lens.max()))
     f = ops.paged_decode_attention(q, kp2, vp2, ip, ix, d**-0.5, kv_scale=sc2, new_kv=(k_new, v_new, out_loc),
@@ -166,7 +169,8 @@ def test_fp8_key_ranges_long_contexts(cuda_device):
 
 
 @pytest.mark.parametrize("dt", ["bf16", "f16"])
-@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256), (64, 8, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (32, 8, 128), (8, 8, 64), (16, 2, 256), (64, 8, 128),
+                                      (24, 12, 128), (32, 16, 64)])
 @pytest.mark.parametrize("planned", [False, True])
 def test_fp8_fused_store_decode_bit_exact(cuda_device, dt, hq, hkv, d, planned):
     """msgl_paged_decode_store_fp8 (the new token quantised and stored inside the
