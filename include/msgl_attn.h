@@ -500,7 +500,8 @@ int msgl_profile_next_launch(void* start_event, void* stop_event);
  * that never reach the host. Walks exactly the entries the attention kernels
  * read (request r: kv_indices[kv_indptr[r] .. + L_r, or ceil(L_r / page_size)
  * page ids]) and never reads past num_indices entries of kv_indices or the
- * [R+1] offsets. status: int64[3] device words, cleared by the call, then
+ * [R+1] offsets; page_size > 1 needs seq_lens, as the attention calls do
+ * (MSGL_ERR_INVALID otherwise). status: int64[3] device words, cleared by the call, then
  * {msgl_meta_error code, request or entry index, offending value} of one
  * violation found (0 = none). Two launches; the caller reads status after
  * synchronising.

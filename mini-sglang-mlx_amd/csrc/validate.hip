@@ -95,6 +95,8 @@ extern "C" int msgl_validate_metadata(const int32_t* kv_indptr, const int32_t* k
   MSGL_CHECK_ARG(status != nullptr && (uintptr_t)status % 8 == 0, "msgl_validate_metadata: status must be int64[3]");
   MSGL_CHECK_ARG(num_reqs >= 0 && page_size >= 1 && num_indices >= 0 && num_slots > 0 && num_tokens >= 0,
                  "msgl_validate_metadata: bad sizes");
+  MSGL_CHECK_ARG(page_size == 1 || seq_lens != nullptr,
+                 "msgl_validate_metadata: page_size > 1 needs seq_lens (as the attention calls do)");
   MSGL_CHECK_ARG(num_reqs == 0 || (kv_indptr != nullptr && (kv_indices != nullptr || num_indices == 0)),
                  "msgl_validate_metadata: null kv_indptr or kv_indices");
   hipStream_t s = (hipStream_t)stream;

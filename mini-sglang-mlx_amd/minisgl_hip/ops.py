@@ -697,6 +697,8 @@ def validate_metadata(
         _check_index(name, t, dev)
     if kv_indptr.dim() != 1 or kv_indptr.shape[0] < 1:
         raise ValueError("kv_indptr must be [R+1]")
+    if page_size > 1 and seq_lens is None:
+        raise ValueError("page_size > 1 needs seq_lens (as the attention calls do)")
     r = kv_indptr.shape[0] - 1
     if seq_lens is not None and seq_lens.shape[0] < r:
         raise ValueError("seq_lens must be [R]")

@@ -202,6 +202,7 @@ def test_host_side_argument_errors():
     assert va(page=0) == _lib.MSGL_ERR_INVALID
     assert va(slots=0) == _lib.MSGL_ERR_INVALID
     assert va(ip=nul) == _lib.MSGL_ERR_INVALID and "null" in _lib.last_error()
+    assert va(page=16) == _lib.MSGL_ERR_INVALID and "seq_lens" in _lib.last_error()  # page ids need lengths
     # store_kv: zero tokens is a no-op; bad row size is unsupported
     assert lib.msgl_store_kv(nul, nul, nul, nul, nul, 0, 8, 128, 10, 1, nul) == _lib.MSGL_OK
     assert lib.msgl_store_kv(16, 16, 16, 16, 16, 4, 1, 3, 10, 1, nul) == _lib.MSGL_ERR_UNSUPPORTED

@@ -74,3 +74,10 @@ def test_decode_split_choice_for_known_lengths():
     assert ops.decode_splits_for(ragged, 8) == ops.default_splits(128, 8, int(ragged.max()))
     assert ops.decode_splits_for(np.full(95, 1144), 8) != 1
     assert ops.decode_splits_for(np.full(128, 3000), 8) != 1
+
+
+def test_validate_metadata_needs_lengths_with_pages():
+    indptr = torch.tensor([0, 2], dtype=torch.int32)
+    ids = torch.zeros(2, dtype=torch.int32)
+    with pytest.raises(ValueError, match="seq_lens"):
+        ops.validate_metadata(indptr, ids, None, num_slots=64, page_size=16)
