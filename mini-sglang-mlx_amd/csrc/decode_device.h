@@ -410,13 +410,24 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
         const int total = (ntile + NST - 1) * 16 * nd;
         const int h0 = kgrp * nwaves;
         const uint32_t sbase = (uint32_t)(uintptr_t)((MSGL_LDS float*)scale_lds);
-        for (int c = wave; c * 64 < total; c += nwaves) {
-          const int idx = c * 64 + lane;
-          if (idx < total) {
-            const int t = idx / nd, d = idx - t * nd;
-            const int h = min(h0 + (d >> 1), p.hkv - 1);  // heads past hkv: an inactive wave's, never read
-            dma4(p.kv_scale + ((int64_t)slots_lds[t] * p.hkv + h) * 2 + (d & 1),
-                 __builtin_amdgcn_readfirstlane(sbase + c * 256));
+        if (nwaves == 4 && (p.hkv & 3) == 0) {
+          // four heads, all present: a token's 32 bytes are two aligned 16-byte transfers
+          const int total16 = total >> 2;
+          for (int c = wave; c * 64 < total16; c += nwaves) {
+            const int idx = c * 64 + lane;
+            if (idx < total16)
+              dma16(p.kv_scale + ((int64_t)slots_lds[idx >> 1] * p.hkv + h0) * 2 + (idx & 1) * 4,
+                    __builtin_amdgcn_readfirstlane(sbase + c * 1024));
+          }
+        } else {
+          for (int c = wave; c * 64 < total; c += nwaves) {
+            const int idx = c * 64 + lane;
+            if (idx < total) {
+              const int t = idx / nd, d = idx - t * nd;
+              const int h = min(h0 + (d >> 1), p.hkv - 1);  // heads past hkv: an inactive wave's, never read
+              dma4(p.kv_scale + ((int64_t)slots_lds[t] * p.hkv + h) * 2 + (d & 1),
+                   __builtin_amdgcn_readfirstlane(sbase + c * 256));
+            }
           }
         }
       }
