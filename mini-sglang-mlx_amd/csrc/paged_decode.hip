@@ -45,6 +45,14 @@
 //  * P.V on the VALU: lane (token sub-row, 16-byte d chunk) accumulates
 //    G x (16/sizeof T) fp32 outputs; P and the rescale factors go through a
 //    small per-wave LDS tile.
+//  * fp8 pools (e4m3 codes, one fp32 K and V scale per slot and kv head): K
+//    codes widen exactly to the query's 16-bit type for the same MFMA, a key's
+//    K scale multiplies its score and its V scale folds into its softmax
+//    weight. A token's scales sit in a 128-byte line of their own, so the
+//    workgroup stages each segment's scales of its kv heads into LDS with LDS
+//    DMA (one request per token and workgroup rather than per wavefront), and
+//    the kv-head groups of one work item run on one XCD, where the second
+//    group finds the line in L2.
 //  * The tile loop is software pipelined: the K/V loads of the next NST-1
 //    tiles are in flight (a ring of register buffers) while one tile is
 //    computed, which is what it takes to keep ~200 KiB of loads in flight per
