@@ -77,3 +77,40 @@ def test_noalloc_rejects_sizes_past_its_array(cuda_device):
     st = lib.msgl_paged_decode_store_noalloc(16, 16, 16, 16, 16, 16, 16, 16, None, 4096, 64, 8, 256, 1, 100,
                                              _lib.MSGL_BF16, 0.1, 64, 16, None)
     assert st == _lib.MSGL_ERR_WORKSPACE and "workspace" in _lib.last_error()
+
+
+def test_noalloc_decode_captured_in_a_graph(cuda_device):
+    """The callers this entry point is for: a decode step captured in a HIP
+    graph (no allocation, no memset inside the library) and replayed three
+    times, with an eager decode of another batch through the same device array
+    between replays; every replay gives the eager call's bits."""
+    lib = _lib.load()
+    batch = 64
+    c, kp, vp, q, kn, vn = _inputs(batch, 200, 2048, 1 << 17, 7, cuda_device)
+    ip, ix, loc = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device), i32(c.out_loc, cuda_device)
+    out_e = torch.empty_like(q)
+    print("case noalloc graph capture", flush=True)
+    assert _noalloc(lib, q, kn, vn, loc, kp, vp, ip, ix, batch, out_e, _lib.current_stream(cuda_device)) == 0
+    torch.cuda.synchronize()
+    pools = (kp.clone(), vp.clone())
+    out_g = torch.full_like(q, float("nan"))
+    graph = torch.cuda.CUDAGraph()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        with torch.cuda.graph(graph, stream=side):
+            st = _noalloc(lib, q, kn, vn, loc, kp, vp, ip, ix, batch, out_g, _lib.current_stream(cuda_device))
+    assert st == _lib.MSGL_OK, _lib.last_error()
+    torch.cuda.current_stream().wait_stream(side)
+    for rep in range(3):
+        out_g.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out_g, out_e), f"replay {rep} differs from the eager call"
+        assert torch.equal(kp, pools[0]) and torch.equal(vp, pools[1]), f"replay {rep}: pools changed"
+        other = torch.empty_like(q[: batch // 2])
+        st = _noalloc(lib, q, kn, vn, loc, kp, vp, ip, ix, batch // 2, other, _lib.current_stream(cuda_device))
+        assert st == _lib.MSGL_OK
+        torch.cuda.synchronize()
+    del graph
+    torch.cuda.empty_cache()
