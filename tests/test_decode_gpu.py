@@ -318,3 +318,34 @@ def test_planned_matches_unplanned(cuda_device, splits):
         assert torch.equal(a, b), f"planned != unplanned at layer {layer}"
     ref = _sampled_ref(q, kp, vp, c, [0, 13, 39], 128**-0.5)
     assert_close(b[[0, 13, 39]], ref, dt, "planned decode")
+
+
+@pytest.mark.parametrize("splits", [None, 1])
+def test_batch_past_plan_staging(cuda_device, splits):
+    """20,000 requests of 0..64 keys: more than the plan kernel stages in LDS
+    (8192 lengths), so it reads the rest from memory. Sampled requests against
+    the oracle (an empty request gives zeros), and the reused plan gives the
+    same bits as the self-planning call."""
+    rng = np.random.default_rng(21)
+    lens = rng.integers(0, 65, size=20000)
+    lens[[5, 9000, 19999]] = 0
+    n = 1 << 21
+    c = workloads.decode_case_from_lens(list(lens), num_slots=n, seed=22)
+    b, hq, hkv, d = len(lens), 16, 8, 128
+    dt = torch.bfloat16
+    kp, vp = _pools(n, hkv, d, dt, 930, cuda_device)
+    q = randn((b, hq, d), 932, dt).to(cuda_device)
+    ip, ix = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    s = splits or ops.default_splits(b, hkv, int(lens.max()))
+    ws = ops.decode_workspace(b, hq, hkv, d, s, cuda_device)
+    print(f"case decode batch 20000 splits={s}", flush=True)
+    a = ops.paged_decode_attention(q, kp, vp, ip, ix, d**-0.5, max_splits=s)
+    ops.paged_decode_plan(ip, None, b, hq, hkv, d, s, ws)
+    p = ops.paged_decode_attention(q, kp, vp, ip, ix, d**-0.5, max_splits=s, workspace=ws, planned=True)
+    torch.cuda.synchronize()
+    assert torch.equal(a, p), "planned != self-planning"
+    pick = [0, 1, 8191, 8192, 8193, 12345, 19998] + [int(np.argmax(lens))]
+    ref = _sampled_ref(q, kp, vp, c, pick, d**-0.5)
+    assert_close(a[pick], ref, dt, "batch 20000")
+    for z in (5, 9000, 19999):
+        assert torch.all(a[z] == 0), f"empty request {z} not zero"
