@@ -156,3 +156,40 @@ def test_planned_matches_unplanned(cuda_device):
                                          max_seq_len=maxs, max_splits=splits, workspace=ws, planned=True)
         torch.cuda.synchronize()
         assert torch.equal(a, b), f"layer {layer}"
+
+
+@pytest.mark.parametrize("splits", [None, 3])
+def test_prefill_many_short_requests(cuda_device, splits):
+    """700 requests of 1..8 new tokens over prefixes of 0..300 (a batch of short
+    prompts and chunk tails): a long work list of one-block items, most rows
+    of each block dead. Sampled requests against the oracle; the plan reused
+    by the planned call gives the same bits."""
+    rng = np.random.default_rng(31)
+    prefix = rng.integers(0, 301, size=700)
+    extend = rng.integers(1, 9, size=700)
+    case = workloads.prefill_case_from_lens(prefix, extend, num_slots=1 << 19, seed=32)
+    hq, hkv, d = 16, 8, 128
+    dt = torch.bfloat16
+    n = case.num_slots
+    kp = randn((n, hkv, d), 50, dt).to(cuda_device)
+    vp = randn((n, hkv, d), 51, dt).to(cuda_device)
+    q = randn((case.num_tokens, hq, d), 52, dt).to(cuda_device)
+    kn = randn((case.num_tokens, hkv, d), 53, dt).to(cuda_device)
+    vn = randn((case.num_tokens, hkv, d), 54, dt).to(cuda_device)
+    ops.store_kv(kn, vn, i32(case.out_loc, cuda_device), kp, vp)
+    qi, ki, kx = (i32(x, cuda_device) for x in (case.q_indptr, case.kv_indptr, case.kv_indices))
+    max_e, max_l = int(case.extend_lens.max()), int(case.seq_lens.max())
+    print(f"case prefill 700 short requests splits={splits}", flush=True)
+    out = ops.prefill_ragged_attention(q, kp, vp, qi, ki, kx, None, d**-0.5, max_extend_len=max_e,
+                                       max_seq_len=max_l, max_splits=splits)
+    s = splits or ops.prefill_default_splits(len(extend), hq, hkv, d, max_e, max_l)
+    ws = ops.prefill_workspace(len(extend), case.num_tokens, max_e, hq, hkv, d, s, cuda_device)
+    ops.prefill_plan(qi, ki, None, num_tokens=case.num_tokens, max_extend_len=max_e, max_seq_len=max_l,
+                     num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, dtype=dt, max_splits=s, workspace=ws)
+    again = ops.prefill_ragged_attention(q, kp, vp, qi, ki, kx, None, d**-0.5, max_extend_len=max_e,
+                                         max_seq_len=max_l, max_splits=s, workspace=ws, planned=True)
+    torch.cuda.synchronize()
+    assert torch.equal(out, again), "planned != self-planning"
+    rows = [0, 1, 350, 698, 699, int(np.argmax(prefix)), int(np.argmin(prefix))]
+    got = torch.cat([out[int(case.q_indptr[i]): int(case.q_indptr[i + 1])] for i in rows])
+    assert_close(got, _oracle(case, q, kn, vn, kp, vp, d, rows=rows), dt, "prefill 700 short requests")
