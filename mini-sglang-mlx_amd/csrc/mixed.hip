@@ -62,8 +62,8 @@ __global__ __launch_bounds__(256) void mixed_merge_kernel(pf::PrefillParams pp, 
 template <typename T, int D, int G>
 int launch_mixed(pf::PrefillParams pp, const dec::DecodeParams& dp, int batch, int max_e, hipStream_t stream) {
   using Geo = pf::G16<D, (int)sizeof(T)>;
-  constexpr int BQ = Geo::ROWS / G;
-  static_assert(pf::THREADS16 == 256 && Geo::ROWS % G == 0, "both bodies run as 4-wavefront workgroups");
+  constexpr int BQ = Geo::ROWS / G;  // as in the prefill body: rows past BQ * G pad the block
+  static_assert(pf::THREADS16 == 256 && G <= Geo::ROWS, "both bodies run as 4-wavefront workgroups");
   pp.nqb = (max_e + BQ - 1) / BQ;
   const int64_t items_pf = (int64_t)pp.hkv * pp.num_reqs * pp.splits * pp.nqb;
   if (items_pf > (int64_t)pp.plan_capacity) {
@@ -98,10 +98,14 @@ int mixed_group(const pf::PrefillParams& pp, const dec::DecodeParams& dp, int ba
   switch (group) {
     case 1: return launch_mixed<T, D, 1>(pp, dp, batch, max_e, s);
     case 2: return launch_mixed<T, D, 2>(pp, dp, batch, max_e, s);
+    case 3: return launch_mixed<T, D, 3>(pp, dp, batch, max_e, s);
     case 4: return launch_mixed<T, D, 4>(pp, dp, batch, max_e, s);
+    case 5: return launch_mixed<T, D, 5>(pp, dp, batch, max_e, s);
+    case 6: return launch_mixed<T, D, 6>(pp, dp, batch, max_e, s);
+    case 7: return launch_mixed<T, D, 7>(pp, dp, batch, max_e, s);
     case 8: return launch_mixed<T, D, 8>(pp, dp, batch, max_e, s);
     default:
-      set_error("msgl_mixed_attention: Hq/Hkv = %d not built (1, 2, 4, 8)", group);
+      set_error("msgl_mixed_attention: Hq/Hkv = %d not built (1-8)", group);
       return MSGL_ERR_UNSUPPORTED;
   }
 }

@@ -356,13 +356,17 @@ static int dispatch_group(const F& f, int group) {
   switch (group) {
     case 1: return f.template run<T, KV, D, 1>();
     case 2: return f.template run<T, KV, D, 2>();
+    case 3: return f.template run<T, KV, D, 3>();
     case 4: return f.template run<T, KV, D, 4>();
+    case 5: return f.template run<T, KV, D, 5>();
+    case 6: return f.template run<T, KV, D, 6>();
+    case 7: return f.template run<T, KV, D, 7>();
     case 8: return f.template run<T, KV, D, 8>();
     case 16:
       if constexpr (!Q8) return f.template run<T, KV, D, 16>();
       [[fallthrough]];
     default:
-      set_error("msgl_paged_decode: Hq/Hkv = %d not built (1, 2, 4, 8%s)", group, Q8 ? " for fp8 pools" : ", 16");
+      set_error("msgl_paged_decode: Hq/Hkv = %d not built (1-8%s)", group, Q8 ? " for fp8 pools" : ", 16");
       return MSGL_ERR_UNSUPPORTED;
   }
 }

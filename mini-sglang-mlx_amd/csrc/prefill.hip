@@ -170,8 +170,8 @@ struct G32 {
 template <int D, int G>
 __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
   constexpr int ROWS = NWAVE * QROWS32;
-  static_assert(ROWS % G == 0, "group must divide the row block");
-  constexpr int BQ = ROWS / G;
+  static_assert(G >= 1 && G <= ROWS, "unsupported group size");
+  constexpr int BQ = ROWS / G;   // query tokens per workgroup; rows past BQ * G pad the block
   constexpr int NDT = D / 16;
   constexpr int KS = G32<D>::KS;
   constexpr int BUF_BYTES = G32<D>::BUF_BYTES;
@@ -353,7 +353,7 @@ __global__ __launch_bounds__(256) void prefill_f32_kernel(PrefillParams p) {
     const int row = wave * QROWS32 + 4 * grp + i;
     const int tok = qb + row / G;
     const float rinv = __shfl(inv, 4 * grp + i);
-    if (tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {
+    if (row < BQ * G && tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {
       float* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
       for (int t = 0; t < NDT; ++t) orow[t * 16 + col] = acc[t][i] * rinv;
@@ -422,11 +422,15 @@ int prefill_group(const PrefillParams& p, int max_e, int group, hipStream_t s) {
   switch (group) {
     case 1: return launch_prefill<T, KV, D, 1>(p, max_e, s);
     case 2: return launch_prefill<T, KV, D, 2>(p, max_e, s);
+    case 3: return launch_prefill<T, KV, D, 3>(p, max_e, s);
     case 4: return launch_prefill<T, KV, D, 4>(p, max_e, s);
+    case 5: return launch_prefill<T, KV, D, 5>(p, max_e, s);
+    case 6: return launch_prefill<T, KV, D, 6>(p, max_e, s);
+    case 7: return launch_prefill<T, KV, D, 7>(p, max_e, s);
     case 8: return launch_prefill<T, KV, D, 8>(p, max_e, s);
     case 16: return launch_prefill<T, KV, D, 16>(p, max_e, s);
     default:
-      set_error("msgl_prefill_ragged: Hq/Hkv = %d not built (1, 2, 4, 8, 16)", group);
+      set_error("msgl_prefill_ragged: Hq/Hkv = %d not built (1-8, 16)", group);
       return MSGL_ERR_UNSUPPORTED;
   }
 }

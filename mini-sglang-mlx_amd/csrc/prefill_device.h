@@ -262,8 +262,9 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
   constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
   using Geo = G16<D, (int)sizeof(KV)>;
   constexpr int ROWS = Geo::ROWS;
-  static_assert(ROWS % G == 0, "group must divide the row block");
-  constexpr int BQ = ROWS / G;  // query tokens per workgroup
+  static_assert(G >= 1 && G <= 32, "unsupported group size");
+  constexpr int BQ = ROWS / G;     // query tokens per workgroup
+  constexpr int RROWS = BQ * G;    // rows holding (token, head) pairs; any rest pads the block
   constexpr int NQF = D / 16;   // 16-wide d steps of the S^T product
   constexpr int NDT = D / 32;   // 32-wide output column tiles
   constexpr int NS = Geo::NS;
@@ -304,7 +305,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
   // A wavefront whose 32 rows all lie past the extend (the last query block of
   // a request) only moves tiles: it issues its share of the LDS transfers and
   // meets every barrier, but computes nothing.
-  const bool live = !MSGL_PREFILL_SKIP_DEAD || qb + wave * 32 / G < E;
+  const bool live = !MSGL_PREFILL_SKIP_DEAD || (wave * 32 < RROWS && qb + wave * 32 / G < E);
   const int my_tok = min(qb + my_row / G, E - 1);
   const int limit = P + my_tok;
   const int lim_lo = __builtin_amdgcn_readfirstlane(limit);  // the wavefront's first row (lane 0)
@@ -744,7 +745,7 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
       const int row = wave * 32 + m;
       const int tok = qb + row / G;
       const float rinv = __shfl(inv, m);
-      if (tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {
+      if (row < RROWS && tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {
         T* orow = out + ((int64_t)(q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) orow[32 * dt + rl] = from_f32<T>(acc[dt][i] * rinv);
@@ -754,14 +755,14 @@ __device__ __forceinline__ void prefill16_body(const PrefillParams& p, int wg) {
     const int64_t base = (int64_t)split * p.num_tokens;
     if (h == 0) {
       const int tok = qb + my_row / G;
-      if (tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens)
+      if (my_row < RROWS && tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens)
         p.part_ml[(base + q0 + tok) * p.hq + kvh * G + my_row % G] = make_float2(m_run, l_row);
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
       const int row = wave * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
       const int tok = qb + row / G;
-      if (tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {  // the workspace holds num_tokens rows
+      if (row < RROWS && tok < E && q0 + tok >= 0 && q0 + tok < p.num_tokens) {  // the workspace holds num_tokens rows
         float* orow = p.part_o + ((base + q0 + tok) * p.hq + kvh * G + row % G) * D;
 #pragma unroll
         for (int dt = 0; dt < NDT; ++dt) orow[32 * dt + rl] = acc[dt][i];
