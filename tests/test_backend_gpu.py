@@ -15,9 +15,9 @@ from minisgl_hip.kvcache import MHAKVCache
 pytestmark = pytest.mark.gpu
 
 
-def _setup(device, dtype, num_layers=3, num_tokens=8192, max_req=8, max_len=1024, page_size=1):
-    cfg = ModelConfig(num_qo_heads=16, num_kv_heads=8, head_dim=128, num_layers=num_layers)
-    kv = MHAKVCache(num_layers, num_tokens, 8, 128, dtype, device)
+def _setup(device, dtype, num_layers=3, num_tokens=8192, max_req=8, max_len=1024, page_size=1, hq=16, hkv=8, d=128):
+    cfg = ModelConfig(num_qo_heads=hq, num_kv_heads=hkv, head_dim=d, num_layers=num_layers)
+    kv = MHAKVCache(num_layers, num_tokens, hkv, d, dtype, device)
     table = np.zeros((max_req, max_len), dtype=np.int32)
     backend = create_attention_backend("hip", cfg, kv, table)
     return cfg, kv, table, backend
@@ -68,11 +68,14 @@ def test_decode_steps_through_backend(cuda_device):
             r.complete_one()
 
 
-def test_prefill_then_decode_through_backend(cuda_device):
+@pytest.mark.parametrize("hq,hkv,d", [(16, 8, 128), (40, 8, 128), (14, 2, 64)])
+def test_prefill_then_decode_through_backend(cuda_device, hq, hkv, d):
     """Chunked prefill (one request with a cached prefix, one without) followed
-    by a decode step, all through prepare_metadata / store_kv / forward."""
+    by a decode step, all through prepare_metadata / store_kv / forward; the
+    Qwen3-0.6B head layout and two whose query-head groups are not powers of two
+    (Qwen3-14B: 40/8, Qwen2.5-0.5B: 14/2 at head_dim 64)."""
     dt = torch.bfloat16
-    cfg, kv, table, backend = _setup(cuda_device, dt, num_layers=2)
+    cfg, kv, table, backend = _setup(cuda_device, dt, num_layers=2, hq=hq, hkv=hkv, d=d)
     rng = np.random.default_rng(1)
     free = rng.permutation(8192).astype(np.int32)
     # request A: 50-token prompt whose first 20 tokens are already cached
@@ -101,10 +104,10 @@ def test_prefill_then_decode_through_backend(cuda_device):
             assert np.array_equal(batch.attn_metadata.kv_indices[0], kvi[0])
         t = len(out_loc)
         for layer in range(cfg.num_layers):
-            q = randn((t, 16, 128), 60 + layer, dt).to(cuda_device)
-            k = randn((t, 8, 128), 70 + layer, dt).to(cuda_device)
-            v = randn((t, 8, 128), 80 + layer, dt).to(cuda_device)
-            print(f"case backend {phase} layer={layer}", flush=True)
+            q = randn((t, hq, d), 60 + layer, dt).to(cuda_device)
+            k = randn((t, hkv, d), 70 + layer, dt).to(cuda_device)
+            v = randn((t, hkv, d), 80 + layer, dt).to(cuda_device)
+            print(f"case backend {phase} {hq}/{hkv}/{d} layer={layer}", flush=True)
             kv.store_kv(k, v, batch.out_loc, layer)
             o = backend.forward(q, k, v, layer, batch)
             torch.cuda.synchronize()
