@@ -14,15 +14,18 @@
 // and elements >= rotary_dim pass through. Arithmetic is fp32 for every
 // storage type; results are rounded once to the storage type.
 //
-// One workgroup of 128 lanes per token (grid-stride over tokens). A rotated
-// row costs rotary_dim/8 pair items (each reads and writes a quad of 4
-// elements in both halves) plus (D - rotary_dim)/4 copy items; a v row costs
-// D/4 copy items. Per token: the position and slot are scalar loads, the
-// cos/sin table is computed once into LDS and shared by all q and k heads,
-// then each lane issues the loads of up to five items before its first store.
-// HBM-bound: q read + written, k and v read + written once each. At a few
-// thousand tokens the whole chunk is in flight at once, so the launch is
-// bounded by two memory round trips per workgroup rather than by bandwidth.
+// One workgroup of 128 lanes per token (grid-stride over tokens). Items are
+// 16 bytes (8 bf16/fp16 or 4 fp32 elements) when the rotated half and the
+// pass-through tail split into such pieces, else 8 bytes: a rotated row costs
+// one pair item per item of its lower half (it reads and writes that item in
+// both halves) plus one copy item per item of the tail; a v row is all copy
+// items. Per token each lane first issues the loads of up to K items (they do
+// not depend on the position), then the position and slot arrive as scalar
+// loads and the cos/sin table is computed once into LDS, shared by all q and k
+// heads; rotation and stores follow. q is read and written, k and v read and
+// written once each. At a few thousand tokens the whole chunk is in flight at
+// once: the launch runs at ~3 TB/s (33 MB in ~11 µs), like a plain copy of
+// its size, rather than at the streaming rate.
 #include "msgl_common.h"
 
 namespace msgl {
@@ -51,12 +54,15 @@ struct RopeParams {
   int rotary_dim;
 };
 
-// Four consecutive elements of storage type T, as fp32.
-template <typename T>
-struct Quad;
+// IB bytes of storage type T (E = IB / sizeof(T) consecutive elements) as fp32:
+// one 16-byte or 8-byte load or store.
+template <typename T, int IB>
+struct Item;
 
-template <>
-struct Quad<float> {
+template <int IB>
+struct Item<float, IB> {
+  static_assert(IB == 16, "fp32 items are four elements");
+  static constexpr int E = 4;
   typedef u32x4 raw_t;
   __device__ __forceinline__ static void unpack(const raw_t& r, float* f) {
 #pragma unroll
@@ -71,13 +77,24 @@ struct Quad<float> {
 };
 
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-
+template <int W>
+struct RawWords;
 template <>
-struct Quad<bf16_t> {
-  typedef u32x2 raw_t;
+struct RawWords<2> {
+  typedef u32x2 type;
+};
+template <>
+struct RawWords<4> {
+  typedef u32x4 type;
+};
+
+template <int IB>
+struct Item<bf16_t, IB> {
+  static constexpr int E = IB / 2;
+  typedef typename RawWords<IB / 4>::type raw_t;
   __device__ __forceinline__ static void unpack(const raw_t& r, float* f) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < IB / 4; ++i) {
       f[2 * i] = __uint_as_float(r[i] << 16);
       f[2 * i + 1] = __uint_as_float(r[i] & 0xffff0000u);
     }
@@ -85,17 +102,19 @@ struct Quad<bf16_t> {
   __device__ __forceinline__ static raw_t pack(const float* f) {
     raw_t r;
 #pragma unroll
-    for (int i = 0; i < 2; ++i) r[i] = (uint32_t)f32_to_bf16(f[2 * i]) | ((uint32_t)f32_to_bf16(f[2 * i + 1]) << 16);
+    for (int i = 0; i < IB / 4; ++i)
+      r[i] = (uint32_t)f32_to_bf16(f[2 * i]) | ((uint32_t)f32_to_bf16(f[2 * i + 1]) << 16);
     return r;
   }
 };
 
-template <>
-struct Quad<f16_t> {
-  typedef u32x2 raw_t;
+template <int IB>
+struct Item<f16_t, IB> {
+  static constexpr int E = IB / 2;
+  typedef typename RawWords<IB / 4>::type raw_t;
   __device__ __forceinline__ static void unpack(const raw_t& r, float* f) {
 #pragma unroll
-    for (int i = 0; i < 2; ++i) {
+    for (int i = 0; i < IB / 4; ++i) {
       f[2 * i] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r[i] & 0xffffu));
       f[2 * i + 1] = (float)__builtin_bit_cast(_Float16, (uint16_t)(r[i] >> 16));
     }
@@ -103,37 +122,36 @@ struct Quad<f16_t> {
   __device__ __forceinline__ static raw_t pack(const float* f) {
     raw_t r;
 #pragma unroll
-    for (int i = 0; i < 2; ++i)
+    for (int i = 0; i < IB / 4; ++i)
       r[i] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[2 * i]) |
              ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)f[2 * i + 1]) << 16);
     return r;
   }
 };
 
-template <typename T>
-__device__ __forceinline__ typename Quad<T>::raw_t ldq(const uint8_t* p) {
-  return *reinterpret_cast<const typename Quad<T>::raw_t*>(p);
+template <typename T, int IB>
+__device__ __forceinline__ typename Item<T, IB>::raw_t ldi(const uint8_t* p) {
+  return *reinterpret_cast<const typename Item<T, IB>::raw_t*>(p);
 }
-template <typename T>
-__device__ __forceinline__ void stq(uint8_t* p, const typename Quad<T>::raw_t& r) {
-  *reinterpret_cast<typename Quad<T>::raw_t*>(p) = r;
+template <typename T, int IB>
+__device__ __forceinline__ void sti(uint8_t* p, const typename Item<T, IB>::raw_t& r) {
+  *reinterpret_cast<typename Item<T, IB>::raw_t*>(p) = r;
 }
 
-// Where item i of a token reads and writes: a pair item rotates quad j of the
-// lower half with quad j of the upper half of one q or k row, a copy item
-// moves one quad of the pass-through tail of a q or k row or of a v row.
+// Where item i of a token reads and writes: a pair item rotates item j of the
+// lower half with item j of the upper half of one q or k row, a copy item
+// moves one item of the pass-through tail of a q or k row or of a v row.
 struct RopeItem {
   const uint8_t* src;
   uint8_t* d0;  // q_out / k_out row (or null)
   uint8_t* d1;  // pool row (or null)
-  int64_t o;    // byte offset of the (lower) quad inside the row
+  int64_t o;    // byte offset of the (lower) item inside the row
   bool pair;
 };
 
-template <typename T>
+template <typename T, int IB>
 __device__ __forceinline__ RopeItem rope_item(const RopeParams& p, int64_t t, int64_t slot, int i, int pairs,
                                               int per_row, int nrot, int vq) {
-  constexpr int QB = 4 * (int)sizeof(T);
   const int64_t row_bytes = (int64_t)p.head_dim * sizeof(T);
   RopeItem it;
   if (i < nrot) {
@@ -146,7 +164,7 @@ __device__ __forceinline__ RopeItem rope_item(const RopeParams& p, int64_t t, in
     it.d0 = isq ? p.q_out + off : (p.k_out ? p.k_out + off : nullptr);
     it.d1 = (!isq && slot >= 0) ? p.k_pool + (slot * p.hkv + h) * row_bytes : nullptr;
     it.pair = j < pairs;
-    it.o = it.pair ? (int64_t)j * QB : (int64_t)p.rotary_dim * sizeof(T) + (int64_t)(j - pairs) * QB;
+    it.o = it.pair ? (int64_t)j * IB : (int64_t)p.rotary_dim * sizeof(T) + (int64_t)(j - pairs) * IB;
   } else {
     const int idx = i - nrot;
     const int h = idx / vq;
@@ -154,90 +172,94 @@ __device__ __forceinline__ RopeItem rope_item(const RopeParams& p, int64_t t, in
     it.d0 = nullptr;
     it.d1 = slot >= 0 ? p.v_pool + (slot * p.hkv + h) * row_bytes : nullptr;
     it.pair = false;
-    it.o = (int64_t)(idx - h * vq) * QB;
+    it.o = (int64_t)(idx - h * vq) * IB;
   }
   return it;
 }
 
-// Items per lane whose loads are all issued before the first store.
-constexpr int kRopeItemsPerLane = 5;
-
-template <typename T>
+// IB-byte items (16 bytes when the rotated half and the tail split into
+// 16-byte pieces, else 8), K per lane whose loads are all issued before the
+// first store. The data loads do not depend on the position, so they are
+// issued before the token's cos/sin table is built: the two memory round
+// trips (position, data) overlap.
+template <typename T, int IB, int K>
 __global__ __launch_bounds__(kRopeThreads) void rope_store_kernel(RopeParams p,
                                                                   const int32_t* __restrict__ positions,
                                                                   const int32_t* __restrict__ slots) {
-  typedef typename Quad<T>::raw_t raw_t;
+  typedef Item<T, IB> I;
+  typedef typename I::raw_t raw_t;
+  constexpr int E = I::E;
   __shared__ float2 cs[kRopeMaxHalf];
   const int half = p.rotary_dim >> 1;
-  const int pairs = half >> 2;  // pair items per rotated row
-  const int per_row = pairs + ((p.head_dim - p.rotary_dim) >> 2);
+  const int pairs = half / E;  // pair items per rotated row
+  const int per_row = pairs + (p.head_dim - p.rotary_dim) / E;
   const int nrot = (p.hq + p.hkv) * per_row;
-  const int vq = p.head_dim >> 2;
+  const int vq = p.head_dim / E;
   // v rows are only touched to store them
   const int n = nrot + ((p.out_loc && p.v_pool) ? p.hkv * vq : 0);
   const int64_t half_bytes = (int64_t)half * sizeof(T);
   // this lane's frequency (half <= kRopeMaxHalf < kRopeThreads), loaded once
   const float freq = (int)threadIdx.x < half ? p.inv_freq[threadIdx.x] : 0.f;
   for (int64_t t = blockIdx.x; t < p.num_tokens; t += gridDim.x) {
-    // the token's position and slot are read-only and uniform: scalar loads
-    // (slots aliases positions when nothing is stored)
-    const float pos = (float)positions[t];
-    const int32_t raw_slot = slots[t];
-    // 1. the token's cos/sin table (one round trip for position and frequency)
-    if (half > 0) {
-      __syncthreads();  // the previous token's readers of cs are done
-      if ((int)threadIdx.x < half) {
-        float sn, cn;
-        sincosf(pos * freq, &sn, &cn);
-        cs[threadIdx.x] = make_float2(cn, sn);
-      }
-      __syncthreads();
-    }
-    // never write outside the pool
-    const int64_t slot = (p.out_loc && raw_slot >= 0 && raw_slot < p.num_slots) ? (int64_t)raw_slot : -1;
-    for (int base = 0; base < n; base += kRopeThreads * kRopeItemsPerLane) {
-      // 2. every load of this lane in flight before any store (items never
+    for (int base = 0; base < n; base += kRopeThreads * K) {
+      // 1. every load of this lane in flight before any store (items never
       //    overlap, so an in-place q_out/k_out is written only after all reads
       //    of the same elements)
-      raw_t lo[kRopeItemsPerLane], hi[kRopeItemsPerLane];
+      raw_t lo[K], hi[K];
 #pragma unroll
-      for (int r = 0; r < kRopeItemsPerLane; ++r) {
+      for (int r = 0; r < K; ++r) {
         const int i = base + r * kRopeThreads + (int)threadIdx.x;
         if (i < n) {
-          const RopeItem it = rope_item<T>(p, t, -1, i, pairs, per_row, nrot, vq);
-          lo[r] = ldq<T>(it.src + it.o);
-          if (it.pair) hi[r] = ldq<T>(it.src + half_bytes + it.o);
+          const RopeItem it = rope_item<T, IB>(p, t, -1, i, pairs, per_row, nrot, vq);
+          lo[r] = ldi<T, IB>(it.src + it.o);
+          if (it.pair) hi[r] = ldi<T, IB>(it.src + half_bytes + it.o);
         }
       }
+      // 2. the token's position and slot (read-only and uniform: scalar loads;
+      //    slots aliases positions when nothing is stored), and on the first
+      //    pass its cos/sin table
+      const float pos = (float)positions[t];
+      const int32_t raw_slot = slots[t];
+      if (base == 0 && half > 0) {
+        __syncthreads();  // the previous token's readers of cs are done
+        if ((int)threadIdx.x < half) {
+          float sn, cn;
+          sincosf(pos * freq, &sn, &cn);
+          cs[threadIdx.x] = make_float2(cn, sn);
+        }
+        __syncthreads();
+      }
+      // never write outside the pool
+      const int64_t slot = (p.out_loc && raw_slot >= 0 && raw_slot < p.num_slots) ? (int64_t)raw_slot : -1;
       // 3. rotate and store
 #pragma unroll
-      for (int r = 0; r < kRopeItemsPerLane; ++r) {
+      for (int r = 0; r < K; ++r) {
         const int i = base + r * kRopeThreads + (int)threadIdx.x;
         if (i >= n) continue;
-        const RopeItem it = rope_item<T>(p, t, slot, i, pairs, per_row, nrot, vq);
+        const RopeItem it = rope_item<T, IB>(p, t, slot, i, pairs, per_row, nrot, vq);
         if (it.pair) {
-          float x0[4], x1[4], a[4], b[4];
-          Quad<T>::unpack(lo[r], x0);
-          Quad<T>::unpack(hi[r], x1);
-          const int e0 = (int)(it.o / (4 * (int)sizeof(T))) * 4;
+          float x0[E], x1[E], a[E], b[E];
+          I::unpack(lo[r], x0);
+          I::unpack(hi[r], x1);
+          const int e0 = (int)(it.o / IB) * E;
 #pragma unroll
-          for (int e = 0; e < 4; ++e) {
+          for (int e = 0; e < E; ++e) {
             const float2 w = cs[e0 + e];
             a[e] = x0[e] * w.x - x1[e] * w.y;
             b[e] = x0[e] * w.y + x1[e] * w.x;
           }
-          const raw_t ra = Quad<T>::pack(a), rb = Quad<T>::pack(b);
+          const raw_t ra = I::pack(a), rb = I::pack(b);
           if (it.d0) {
-            stq<T>(it.d0 + it.o, ra);
-            stq<T>(it.d0 + half_bytes + it.o, rb);
+            sti<T, IB>(it.d0 + it.o, ra);
+            sti<T, IB>(it.d0 + half_bytes + it.o, rb);
           }
           if (it.d1) {
-            stq<T>(it.d1 + it.o, ra);
-            stq<T>(it.d1 + half_bytes + it.o, rb);
+            sti<T, IB>(it.d1 + it.o, ra);
+            sti<T, IB>(it.d1 + half_bytes + it.o, rb);
           }
         } else {
-          if (it.d0) stq<T>(it.d0 + it.o, lo[r]);
-          if (it.d1) stq<T>(it.d1 + it.o, lo[r]);
+          if (it.d0) sti<T, IB>(it.d0 + it.o, lo[r]);
+          if (it.d1) sti<T, IB>(it.d1 + it.o, lo[r]);
         }
       }
     }
@@ -273,10 +295,22 @@ int launch_rope(const RopeParams& p, int32_t dtype, void* stream, const char* wh
   const int64_t blocks = p.num_tokens < kRopeMaxBlocks ? p.num_tokens : kRopeMaxBlocks;
   const int32_t* slots = p.out_loc ? p.out_loc : p.positions;
   hipStream_t s = (hipStream_t)stream;
+  // 16-byte items when the rotated half and the pass-through tail split into
+  // 16-byte pieces (and the tensors allow it), else 8-byte items
+  const bool wide = es == 4 || ((p.rotary_dim / 2) % 8 == 0 && (p.head_dim - p.rotary_dim) % 8 == 0 &&
+                                ((uintptr_t)p.q | (uintptr_t)p.q_out | (uintptr_t)p.k | (uintptr_t)p.k_out |
+                                 (uintptr_t)p.v | (uintptr_t)p.k_pool | (uintptr_t)p.v_pool) % 16 == 0);
+  const dim3 g((unsigned)blocks), b(kRopeThreads);
   switch (dtype) {
-    case MSGL_F32: hipLaunchKernelGGL(rope_store_kernel<float>, dim3((unsigned)blocks), dim3(kRopeThreads), 0, s, p, p.positions, slots); break;
-    case MSGL_BF16: hipLaunchKernelGGL(rope_store_kernel<bf16_t>, dim3((unsigned)blocks), dim3(kRopeThreads), 0, s, p, p.positions, slots); break;
-    default: hipLaunchKernelGGL(rope_store_kernel<f16_t>, dim3((unsigned)blocks), dim3(kRopeThreads), 0, s, p, p.positions, slots); break;
+    case MSGL_F32: hipLaunchKernelGGL((rope_store_kernel<float, 16, 4>), g, b, 0, s, p, p.positions, slots); break;
+    case MSGL_BF16:
+      if (wide) hipLaunchKernelGGL((rope_store_kernel<bf16_t, 16, 4>), g, b, 0, s, p, p.positions, slots);
+      else hipLaunchKernelGGL((rope_store_kernel<bf16_t, 8, 5>), g, b, 0, s, p, p.positions, slots);
+      break;
+    default:
+      if (wide) hipLaunchKernelGGL((rope_store_kernel<f16_t, 16, 4>), g, b, 0, s, p, p.positions, slots);
+      else hipLaunchKernelGGL((rope_store_kernel<f16_t, 8, 5>), g, b, 0, s, p, p.positions, slots);
+      break;
   }
   MSGL_CHECK_LAUNCH(what);
   return MSGL_OK;
