@@ -33,12 +33,12 @@ Nested workloads (also runnable alone, one JSON line each):
   mixed     one continuous-batching step, Qwen3-8B heads, page 16, 8M-slot pool:
             128 decode requests (context U[512, 32768]) + chunks of 1024 over
             prefixes 0 and 8192, indices built on the GPU from the page table
-Other workloads (alone only):
   decode_fp8  the headline decode over fp8 e4m3 pools with one scale
             per slot and kv head (quantising store + fp8 decode per layer)
   prefill_fp8 the prefill workload over fp8 e4m3 pools
   rope      rotate-half RoPE of q and k fused with the KV store over the
             prefill workload's 2040 packed tokens (Qwen3-0.6B heads), 28 layers
+Other workloads (alone only):
   ceilings  a 1 GiB device copy and an 8192^3 bf16 GEMM
 """
 
@@ -192,7 +192,9 @@ def _traffic_ratio(name: str, algorithmic: float):
 def nested_workloads(args, dev):
     """The other measured configurations of the attention path, each on its own
     pools (freed before the next): Qwen3-8B-head decode at batch 256 and page 16,
-    the 16-request ragged prefill, and the mixed continuous-batching step."""
+    the 16-request ragged prefill, the mixed continuous-batching step, and the
+    extensions around the path: decode and prefill over an fp8 KV cache and the
+    fused RoPE + KV store."""
     import torch
 
     out = {}
@@ -200,6 +202,10 @@ def nested_workloads(args, dev):
         ("decode_8b_b256_ctx8k_page16", bench_decode8b, "paged_decode_8b_b256_ctx8k_page16_traffic.txt"),
         ("prefill_ragged_16req", bench_prefill, "prefill_ragged_16req_traffic.txt"),
         ("mixed_step_8b_page16", bench_mixed, "mixed_step_8b_page16_traffic.txt"),
+        ("decode_fp8_b128_ctx2k", bench_decode_fp8, "paged_decode_fp8_b128_ctx2k_traffic.txt"),
+        ("prefill_ragged_16req_fp8", lambda a, d: bench_prefill(a, d, fp8=True),
+         "prefill_ragged_16req_fp8_traffic.txt"),
+        ("rope_store_kv_prefill2040", bench_rope, "rope_store_kv_prefill2040_traffic.txt"),
     ):
         torch.cuda.empty_cache()
         print(f"# workload {name}", file=sys.stderr, flush=True)
@@ -208,7 +214,8 @@ def nested_workloads(args, dev):
         entry = {"workload": cfg["workload"], "metric": line["metric"], "value": line["value"],
                  "unit": line["unit"], "ms_per_step": line["ms_per_step"], "roofline": line["roofline"]}
         entry.update({k: v for k, v in cfg.items() if k != "workload"})
-        alg = cfg.get("bytes_per_step") or cfg.get("kernel_bytes")
+        alg = (cfg.get("bytes_per_step") or cfg.get("kernel_bytes") or cfg.get("bytes_per_layer")
+               or cfg.get("bytes_per_launch"))
         entry["traffic_ratio"] = _traffic_ratio(profile, alg) if alg else None
         out[name] = entry
         torch.cuda.synchronize()
