@@ -392,3 +392,13 @@ def test_backend_with_fp8_cache(cuda_device):
                 r.complete_one()
     finally:
         set_global_ctx(None)
+
+
+@pytest.mark.parametrize("splits", [1, 3])
+def test_fp8_prefill_requests_without_extend(cuda_device, splits):
+    """fp8 pools: requests with no extend tokens between real ones leave the
+    other requests' outputs equal to the oracle's."""
+    case = workloads.prefill_case_from_lens([100, 50, 0, 20, 2000], [37, 0, 5, 0, 130], num_slots=8192, seed=5)
+    print(f"case fp8 prefill empty extends splits={splits}", flush=True)
+    q, kp, vp, sc, out = _fp8_prefill(case, 16, 8, 128, torch.bfloat16, cuda_device, 70, splits=splits)
+    assert_close(out, _fp8_prefill_oracle(case, q, kp, vp, sc, 128), torch.bfloat16, "fp8 prefill empty extends")

@@ -193,3 +193,28 @@ def test_prefill_many_short_requests(cuda_device, splits):
     rows = [0, 1, 350, 698, 699, int(np.argmax(prefix)), int(np.argmin(prefix))]
     got = torch.cat([out[int(case.q_indptr[i]): int(case.q_indptr[i + 1])] for i in rows])
     assert_close(got, _oracle(case, q, kn, vn, kp, vp, d, rows=rows), dt, "prefill 700 short requests")
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16"])
+@pytest.mark.parametrize("splits", [1, 3])
+def test_prefill_requests_without_extend(cuda_device, dtype, splits):
+    """Requests with no extend tokens (repeated q offsets) between real ones:
+    none of their rows is computed or written and the others match the oracle.
+    The scheduler never forms such a batch (scheduler/prefill.py:67-83: every
+    chunk takes at least one token), but a caller's metadata may."""
+    dt = DTYPES[dtype]
+    case = workloads.prefill_case_from_lens([100, 50, 0, 20, 2000], [37, 0, 5, 0, 130], num_slots=8192, seed=5)
+    hq, hkv, d = 16, 8, 128
+    kp = randn((case.num_slots, hkv, d), 60, dt).to(cuda_device)
+    vp = randn((case.num_slots, hkv, d), 61, dt).to(cuda_device)
+    q = randn((case.num_tokens, hq, d), 62, dt).to(cuda_device)
+    kn = randn((case.num_tokens, hkv, d), 63, dt).to(cuda_device)
+    vn = randn((case.num_tokens, hkv, d), 64, dt).to(cuda_device)
+    ops.store_kv(kn, vn, i32(case.out_loc, cuda_device), kp, vp)
+    print(f"case prefill empty extends {dtype} splits={splits}", flush=True)
+    out = ops.prefill_ragged_attention(q, kp, vp, i32(case.q_indptr, cuda_device), i32(case.kv_indptr, cuda_device),
+                                       i32(case.kv_indices, cuda_device), None, d**-0.5,
+                                       max_extend_len=int(case.extend_lens.max()),
+                                       max_seq_len=int(case.seq_lens.max()), max_splits=splits)
+    torch.cuda.synchronize()
+    assert_close(out, _oracle(case, q, kn, vn, kp, vp, d), dt, f"prefill empty extends {dtype} splits={splits}")
