@@ -25,6 +25,8 @@ CASES = [  # (T, H, D, rotary_dim, base, scaling)
     (19, 8, 128, 64, 1e4, None),  # partial rotary: the upper half passes through
     (11, 4, 256, 256, 5e5, LLAMA3),
     (9, 2, 128, 128, 1e4, {"rope_type": "linear", "factor": 4.0}),
+    (13, 4, 32, 24, 1e4, None),  # half the rotary dim not a multiple of 8: 8-byte items for 16-bit types
+    (7, 3, 36, 32, 1e4, None),  # a pass-through tail of 4 elements
 ]
 
 
@@ -64,9 +66,13 @@ def test_rope_in_place(cuda_device):
 
 
 @pytest.mark.parametrize("dt", ["f32", "bf16"])
-def test_rope_store_kv_matches_oracle(cuda_device, dt):
+@pytest.mark.parametrize("d,rot", [(128, 128), (32, 24), (36, 32)])
+def test_rope_store_kv_matches_oracle(cuda_device, dt, d, rot):
+    """Qwen3's full rotation (16-byte items), and two shapes the 16-bit kernel
+    moves in 8-byte items: half the rotary dim not a multiple of 8 (24), and a
+    pass-through tail of 4 elements (36 / 32)."""
     dtype = DTYPES[dt]
-    t, hq, hkv, d, n = 300, 32, 8, 128, 4096
+    t, hq, hkv, n = 300, 32, 8, 4096
     q = randn((t, hq, d), 10, dtype).to(cuda_device)
     k = randn((t, hkv, d), 11, dtype).to(cuda_device)
     v = randn((t, hkv, d), 12, dtype).to(cuda_device)
@@ -75,27 +81,27 @@ def test_rope_store_kv_matches_oracle(cuda_device, dt):
     kp, vp = kp0.clone(), vp0.clone()
     loc = np.random.default_rng(15).permutation(n)[:t]
     pos = _positions(t, 16)
-    inv = rope_inv_freq(d, 1e6).to(cuda_device)
-    print(f"case rope_store_kv {dt}", flush=True)
+    inv = rope_inv_freq(rot, 1e6).to(cuda_device)
+    print(f"case rope_store_kv {dt} d={d} rot={rot}", flush=True)
     k_out = torch.empty_like(k)
-    q_out = ops.rope_store_kv(q, k, v, i32(pos, cuda_device), i32(loc, cuda_device), kp, vp, inv, d, k_out=k_out)
+    q_out = ops.rope_store_kv(q, k, v, i32(pos, cuda_device), i32(loc, cuda_device), kp, vp, inv, rot, k_out=k_out)
     torch.cuda.synchronize()
-    oinv = oracle.rope_inv_freq(d, 1e6)
-    assert_close(q_out, oracle.rope(to_np64(q), pos, d, oinv), dtype, "rotated q")
+    oinv = oracle.rope_inv_freq(rot, 1e6)
+    assert_close(q_out, oracle.rope(to_np64(q), pos, rot, oinv), dtype, "rotated q")
     loc_t = torch.from_numpy(loc).to(cuda_device)
-    assert_close(kp[loc_t], oracle.rope(to_np64(k), pos, d, oinv), dtype, "stored rotated k")
+    assert_close(kp[loc_t], oracle.rope(to_np64(k), pos, rot, oinv), dtype, "stored rotated k")
     assert torch.equal(kp[loc_t], k_out)  # k_out is exactly what was stored
     assert torch.equal(vp[loc_t], v)  # v is stored unrotated, bit-exact
     # same arithmetic as the plain rotation kernel, bit for bit
     posd = i32(pos, cuda_device)
-    assert torch.equal(q_out, ops.rope(q, posd, inv, d))
-    assert torch.equal(k_out, ops.rope(k, posd, inv, d))
+    assert torch.equal(q_out, ops.rope(q, posd, inv, rot))
+    assert torch.equal(k_out, ops.rope(k, posd, inv, rot))
     rest = torch.ones(n, dtype=torch.bool, device=cuda_device)
     rest[loc_t] = False
     assert torch.equal(kp[rest], kp0[rest]) and torch.equal(vp[rest], vp0[rest])
     # in place on q and k
     q2, k2 = q.clone(), k.clone()
-    ops.rope_store_kv(q2, k2, v, posd, i32(loc, cuda_device), kp, vp, inv, d, q_out=q2, k_out=k2)
+    ops.rope_store_kv(q2, k2, v, posd, i32(loc, cuda_device), kp, vp, inv, rot, q_out=q2, k_out=k2)
     torch.cuda.synchronize()
     assert torch.equal(q2, q_out) and torch.equal(k2, k_out)
 
