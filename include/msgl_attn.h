@@ -447,10 +447,12 @@ int msgl_prefill_ragged_fp8_planned(const void* q, const void* k_pool, const voi
  * msgl_prefill_ragged_planned with the same arguments, whose work lists
  * msgl_paged_decode_plan (into dec_workspace) and msgl_prefill_plan (into
  * pf_workspace) must have built for these indices and sizes. Both parts share
- * the pools, head counts, head_dim (64 or 128), page size, dtype (bf16/fp16)
- * and scale; q_dec/out_dec are [num_decode, Hq, D], q_pf/out_pf the packed
- * [num_tokens, Hq, D] the prefill's q_indptr indexes (they may be views of one
- * packed batch). With no request of one phase it runs the other's planned call.
+ * the pools, head counts, head_dim, page size, dtype and scale; q_dec/out_dec
+ * are [num_decode, Hq, D], q_pf/out_pf the packed [num_tokens, Hq, D] the
+ * prefill's q_indptr indexes (they may be views of one packed batch). The one
+ * launch is built for bf16/fp16, head_dim 64 and 128 and Hq/Hkv 1 to 8; other
+ * shapes, and batches with no request of one phase, run the two planned calls
+ * in turn on the stream (the same results).
  */
 int msgl_mixed_attention(const void* q_dec, const void* k_new, const void* v_new, const int32_t* out_loc,
                          const int32_t* dec_kv_indptr, const int32_t* dec_kv_indices, const int32_t* dec_seq_lens,

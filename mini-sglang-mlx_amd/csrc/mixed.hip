@@ -161,7 +161,15 @@ extern "C" int msgl_mixed_attention(const void* q_dec, const void* k_new, const 
   using namespace msgl;
   clear_error();
   MSGL_CHECK_ARG(num_decode >= 0 && num_prefill >= 0, "msgl_mixed_attention: request counts must be >= 0");
-  if (num_decode == 0 || num_prefill == 0 || max_extend_len == 0 || num_tokens == 0) {  // one phase only
+  // The single launch is built for 16-bit q, head_dim 64 and 128 and Hq/Hkv 1
+  // to 8 (a larger group's decode accumulators do not fit beside the prefill
+  // body's registers). Other shapes, and batches of one phase, run the phases
+  // as launches of their own on the stream: the same results as the decode and
+  // prefill calls, which touch disjoint slots (a request is in one phase).
+  const int group = num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0 ? num_qo_heads / num_kv_heads : 0;
+  const bool one_launch = (dtype == MSGL_BF16 || dtype == MSGL_F16) && (head_dim == 64 || head_dim == 128) &&
+                          group >= 1 && group <= 8;
+  if (num_decode == 0 || num_prefill == 0 || max_extend_len == 0 || num_tokens == 0 || !one_launch) {
     int st = MSGL_OK;
     if (num_prefill > 0)
       st = msgl_prefill_ragged_planned(q_pf, k_pool, v_pool, q_indptr, pf_kv_indptr, pf_kv_indices, pf_seq_lens,
@@ -179,10 +187,6 @@ extern "C" int msgl_mixed_attention(const void* q_dec, const void* k_new, const 
                                            dtype, scale, dec_max_splits, out_dec, dec_workspace, dec_workspace_bytes,
                                            stream);
     return st;
-  }
-  if (dtype != MSGL_BF16 && dtype != MSGL_F16) {
-    set_error("msgl_mixed_attention: bf16 or fp16 only (dtype %d)", dtype);
-    return MSGL_ERR_UNSUPPORTED;
   }
   MSGL_CHECK_ARG((k_new == nullptr) == (v_new == nullptr) && (k_new == nullptr || out_loc != nullptr),
                  "msgl_mixed_attention: k_new, v_new and out_loc go together");
@@ -206,7 +210,6 @@ extern "C" int msgl_mixed_attention(const void* q_dec, const void* k_new, const 
   // items (measured slower), and the list keeps the longest items first.
   dp.balanced = false;
   dp.shared_head = false;  // one workgroup per work item here (max_splits == 1 runs the per-head-group form)
-  const int group = num_qo_heads / num_kv_heads;
   hipStream_t s = (hipStream_t)stream;
   return dtype == MSGL_BF16 ? mixed_dim<bf16_t>(pp, dp, num_decode, max_extend_len, head_dim, group, s)
                             : mixed_dim<f16_t>(pp, dp, num_decode, max_extend_len, head_dim, group, s);

@@ -131,7 +131,7 @@ def test_fp8_groups(cuda_device, hq, hkv, d, splits):
     assert_close(out, _fp8_prefill_oracle(case, q, kp, vp, sc, d), dt, f"fp8 prefill groups {hq}/{hkv}/{d}")
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(24, 8, 128), (40, 8, 128), (28, 4, 128), (14, 2, 64)])
+@pytest.mark.parametrize("hq,hkv,d", [(24, 8, 128), (40, 8, 128), (28, 4, 128), (14, 2, 64), (32, 2, 128)])
 def test_mixed_groups(cuda_device, hq, hkv, d):
     """msgl_mixed_attention: bit-identical to the decode and prefill calls run in
     turn; every request against the oracle (head_dim 128)."""
