@@ -183,7 +183,8 @@ def test_host_side_argument_errors():
         16, 16, 16, 16, nul, npf, 64, 32, 0, 1, 16, 256, 1 << 30,
         16, 16, 16, 8, 128, 1, 100, dtype, 0.1, nul)
     assert mx(nd=-1) == _lib.MSGL_ERR_INVALID
-    assert mx(dtype=0) == _lib.MSGL_ERR_UNSUPPORTED and "bf16 or fp16" in _lib.last_error()
+    # an unknown dtype is rejected before any launch (fp32 now runs the phases apart, which would launch)
+    assert mx(dtype=9) == _lib.MSGL_ERR_UNSUPPORTED and "dtype" in _lib.last_error()
     assert mx(loc=nul) == _lib.MSGL_ERR_INVALID and "out_loc" in _lib.last_error()
     assert mx(kn=24) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
     # fp8 prefill: (q, kp, vp, kv_scale, q_indptr, kv_indptr, kv_indices, seq_lens, R, T, maxE, maxL, Hq, Hkv, D,
