@@ -115,6 +115,10 @@ __device__ __forceinline__ int64_t balanced_range(int64_t ttot, int max_len, int
 // shorter ranges measured slower on MI355X than per-request chunks (each chunk
 // pays its slot staging, fold and partial store, and the merge reads more
 // partials), longer ones faster (ragged long contexts leave no tail).
+// 0: no key-range form; split per request in chunks of one batch-wide length.
+#ifndef MSGL_DECODE_BALANCED
+#define MSGL_DECODE_BALANCED 1
+#endif
 #ifndef MSGL_DECODE_BALANCED_MIN_RANGE
 #define MSGL_DECODE_BALANCED_MIN_RANGE 2048
 #endif
@@ -845,6 +849,32 @@ int decode_params(const char* fn, bool planned, const void* q, const void* k_new
 // Workgroups of the decode launch (p.nranges key ranges x p.ngrp kv-head
 // groups when balanced, else one per plan item). (paged_decode.hip)
 int64_t decode_items(const DecodeParams& p);
+
+// The work-list launch (paged_decode.hip).
+int launch_decode_plan(const DecodeParams& p, hipStream_t stream);
+
+// A request to the instantiation that (query type, pool type, head_dim, query-
+// head group) selects: the decode launch (plan unless p->planned, attention,
+// merge), the merge launch alone, or a property of the instantiation.
+enum DecodeOpKind { kOpLaunch = 0, kOpMerge = 1, kOpShared = 2, kOpResident = 3 };
+struct DecodeOp {
+  DecodeOpKind kind;
+  const DecodeParams* p;  // kOpLaunch, kOpMerge
+  int batch;              // kOpLaunch, kOpMerge
+  hipStream_t stream;     // kOpLaunch, kOpMerge
+  int nwaves;             // kOpResident: wavefronts per workgroup
+  int* resident;          // kOpResident: workgroups the device holds at once
+  bool* flag;             // kOpShared: the shared-head form is built; kOpResident: the key-range form is built
+};
+
+// op applied to the instantiations of one (query, pool) type pair, each pair
+// built in a translation unit of its own (inst/decode_*.hip over
+// decode_launch.h).
+int decode_op_f32(const DecodeOp& op, int head_dim, int group);
+int decode_op_bf16(const DecodeOp& op, int head_dim, int group);
+int decode_op_f16(const DecodeOp& op, int head_dim, int group);
+int decode_op_bf16_fp8(const DecodeOp& op, int head_dim, int group);
+int decode_op_f16_fp8(const DecodeOp& op, int head_dim, int group);
 
 }  // namespace dec
 }  // namespace msgl

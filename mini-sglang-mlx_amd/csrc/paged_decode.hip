@@ -64,54 +64,8 @@
 
 #include "decode_device.h"
 
-// 0: no key-range form; split per request in chunks of one batch-wide length.
-#ifndef MSGL_DECODE_BALANCED
-#define MSGL_DECODE_BALANCED 1
-#endif
-
 namespace msgl {
 using namespace dec;
-
-// Occupancy floor: 16-bit queries with D <= 128 and up to 2 query heads per kv
-// head fit 3 wavefronts per SIMD (168 VGPRs) without spilling, which keeps
-// more K/V loads in flight per CU; the rest keep MSGL_DECODE_MIN_WAVES.
-#ifndef MSGL_DECODE_G2_MIN_WAVES
-#define MSGL_DECODE_G2_MIN_WAVES 3
-#endif
-template <typename T, int D, int G>
-constexpr int decode_min_waves() {
-  return (sizeof(T) == 2 && D <= 128 && G <= 2 && MSGL_DECODE_MIN_WAVES < MSGL_DECODE_G2_MIN_WAVES)
-             ? MSGL_DECODE_G2_MIN_WAVES
-             : MSGL_DECODE_MIN_WAVES;
-}
-
-// Instantiations with the key-range form built in: the shapes where its chunk
-// loop (10-25 more VGPRs) leaves the occupancy as it is -- 16-bit queries,
-// head_dim 128, up to 8 query heads per kv head (2 or 4 over fp8 pools).
-template <typename T, typename KV, int D, int G>
-constexpr bool decode_ranges() {
-  constexpr bool q8 = std::is_same<KV, fp8e4m3>::value;
-  return MSGL_DECODE_BALANCED && sizeof(T) == 2 && D == 128 && (q8 ? (G == 2 || G == 4) : G <= 8);
-}
-
-template <typename T, typename KV, int D, int G>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(decode_min_waves<T, D, G>())))
-void paged_decode_kernel(DecodeParams p) {
-  paged_decode_body<T, KV, D, G, decode_ranges<T, KV, D, G>()>(p, blockIdx.x);
-}
-
-// The shared-head form (max_splits == 1): kSharedWaves wavefronts per
-// (request, kv head), no merge.
-template <typename T, typename KV, int D, int G>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(decode_min_waves<T, D, G>())))
-void paged_decode_shared_kernel(DecodeParams p) {
-  if constexpr (decode_shared<T, KV, D, G>()) paged_decode_body<T, KV, D, G, false, true>(p, blockIdx.x);
-}
-
-template <typename T, int D, int G>
-__global__ __launch_bounds__(256) void paged_decode_merge_kernel(DecodeParams p, int batch) {
-  paged_decode_merge_body<T, D, G>(p, batch, blockIdx.x);
-}
 
 // Plan for paged_decode_kernel, one workgroup. When key ranges are allowed
 // (max_splits > 1): tok_off[b] = sum of L over the requests before b
@@ -251,156 +205,38 @@ __global__ __launch_bounds__(kPlanThreads) void paged_decode_plan_kernel(DecodeP
   }
 }
 
-template <typename T, typename KV, int D, int G>
-static int launch_decode(const DecodeParams& p_in, int batch, hipStream_t stream) {
-  DecodeParams p = p_in;
-  const int nwaves = p.hkv < MSGL_DECODE_WAVES_PER_WG ? p.hkv : MSGL_DECODE_WAVES_PER_WG;
-  const size_t lds = decode_lds_bytes<KV, D>(nwaves);
-  if (!p.planned) {
-    hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
-    MSGL_CHECK_LAUNCH("msgl_paged_decode (plan)");
-  }
-  if constexpr (decode_shared<T, KV, D, G>()) {
-    if (p.shared_head) {  // one launch, no merge: kSharedWaves wavefronts per (request, kv head)
-      if (std::is_same<KV, fp8e4m3>::value && p.k_new != nullptr) {
-        // fp8 pools: the quantising store first (the waves of a workgroup do not
-        // read back a slot another of them wrote), then the decode reads it
-        const int st = msgl_store_kv_fp8(p.k_new, p.v_new, p.out_loc, p.k_pool_w, p.v_pool_w, p.kv_scale_w, batch,
-                                         p.hkv, D, p.num_slots, std::is_same<T, bf16_t>::value ? MSGL_BF16 : MSGL_F16,
-                                         stream);
-        if (st != MSGL_OK) return st;
-        p.k_new = p.v_new = nullptr;
-        p.out_loc = nullptr;
-      }
-      launch_main(paged_decode_shared_kernel<T, KV, D, G>, dim3((unsigned)(dec::decode_items(p) * p.hpg)),
-                  dim3(64 * kSharedWaves), decode_shared_lds_bytes<KV, D, G>(), stream, p);
-      MSGL_CHECK_LAUNCH("msgl_paged_decode");
-      return MSGL_OK;
-    }
-  }
-  launch_main(paged_decode_kernel<T, KV, D, G>, dim3((unsigned)dec::decode_items(p)), dim3(64 * nwaves), lds, stream,
-              p);
-  MSGL_CHECK_LAUNCH("msgl_paged_decode");
-  if (p.max_splits > 1 && !p.skip_merge) {
-    const int units = batch * p.hkv;
-    hipLaunchKernelGGL((paged_decode_merge_kernel<T, D, G>), dim3((units + 3) / 4), dim3(256), 0, stream, p, batch);
-    MSGL_CHECK_LAUNCH("msgl_paged_decode (merge)");
-  }
+int dec::launch_decode_plan(const DecodeParams& p, hipStream_t stream) {
+  hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, p);
+  MSGL_CHECK_LAUNCH("msgl_paged_decode (plan)");
   return MSGL_OK;
 }
 
-// The split-K merge launch on its own (msgl_paged_decode_merge).
-struct MergeLaunch {
-  const DecodeParams& p;
-  int batch;
-  hipStream_t stream;
-  template <typename T, typename KV, int D, int G>
-  int run() const {
-    const int units = batch * p.hkv;
-    launch_main(paged_decode_merge_kernel<T, D, G>, dim3((units + 3) / 4), dim3(256), 0, stream, p, batch);
-    MSGL_CHECK_LAUNCH("msgl_paged_decode_merge");
-    return MSGL_OK;
-  }
-};
-
-// Whether the instantiation has the shared-head form (max_splits == 1).
-struct SharedOK {
-  bool* out;
-  template <typename T, typename KV, int D, int G>
-  int run() const {
-    *out = decode_shared<T, KV, D, G>();
-    return MSGL_OK;
-  }
-};
-
-struct Launch {
-  const DecodeParams& p;
-  int batch;
-  hipStream_t stream;
-  template <typename T, typename KV, int D, int G>
-  int run() const { return launch_decode<T, KV, D, G>(p, batch, stream); }
-};
-
-// Workgroups of paged_decode_kernel<T, KV, D, G> the device holds at once
-// (occupancy x CUs), measured once per process and shape.
-struct Resident {
-  int nwaves;
-  int* out;
-  bool* ranges;  // the instantiation has the key-range form
-  template <typename T, typename KV, int D, int G>
-  int run() const {
-    *ranges = decode_ranges<T, KV, D, G>();
-    static std::atomic<int> cached[MSGL_DECODE_WAVES_PER_WG + 1];  // per process: one device type
-    int c = cached[nwaves].load(std::memory_order_relaxed);
-    if (c == 0) {
-      int per_cu = 0, dev = 0, cus = 0;
-      if (hipOccupancyMaxActiveBlocksPerMultiprocessor(
-              &per_cu, reinterpret_cast<const void*>(&paged_decode_kernel<T, KV, D, G>), 64 * nwaves,
-              decode_lds_bytes<KV, D>(nwaves)) != hipSuccess ||
-          hipGetDevice(&dev) != hipSuccess ||
-          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) {
-        set_error("msgl_paged_decode: occupancy query failed: %s", hipGetErrorString(hipGetLastError()));
-        return MSGL_ERR_HIP;
-      }
-      c = per_cu * cus > 0 ? per_cu * cus : 1;
-      cached[nwaves].store(c, std::memory_order_relaxed);
-    }
-    *out = c;
-    return MSGL_OK;
-  }
-};
-
-template <typename T, typename KV, int D, typename F>
-static int dispatch_group(const F& f, int group) {
-  constexpr bool Q8 = std::is_same<KV, fp8e4m3>::value;
-  switch (group) {
-    case 1: return f.template run<T, KV, D, 1>();
-    case 2: return f.template run<T, KV, D, 2>();
-    case 3: return f.template run<T, KV, D, 3>();
-    case 4: return f.template run<T, KV, D, 4>();
-    case 5: return f.template run<T, KV, D, 5>();
-    case 6: return f.template run<T, KV, D, 6>();
-    case 7: return f.template run<T, KV, D, 7>();
-    case 8: return f.template run<T, KV, D, 8>();
-    case 16:
-      if constexpr (!Q8) return f.template run<T, KV, D, 16>();
-      [[fallthrough]];
-    default:
-      set_error("msgl_paged_decode: Hq/Hkv = %d not built (1-8%s)", group, Q8 ? " for fp8 pools" : ", 16");
-      return MSGL_ERR_UNSUPPORTED;
-  }
-}
-
-template <typename T, typename KV = T, typename F>
-static int dispatch_dim(const F& f, int head_dim, int group) {
-  switch (head_dim) {
-    case 64: return dispatch_group<T, KV, 64>(f, group);
-    case 128: return dispatch_group<T, KV, 128>(f, group);
-    case 256: return dispatch_group<T, KV, 256>(f, group);
-    default:
-      set_error("msgl_paged_decode: head_dim %d not built (64, 128, 256)", head_dim);
-      return MSGL_ERR_UNSUPPORTED;
-  }
-}
-
-// The kernel instantiation of (dtype, fp8 pool, head_dim, group) applied to f.
-template <typename F>
-static int dispatch(const F& f, int dtype, bool q8, int head_dim, int group, const char* fn) {
+// The instantiation of (dtype, fp8 pool, head_dim, group) applied to op; each
+// (query, pool) type pair is built in a translation unit of its own.
+static int dispatch(const DecodeOp& op, int dtype, bool q8, int head_dim, int group, const char* fn) {
   if (q8) {  // fp8 e4m3 pools with per-(slot, kv head) scales
     switch (dtype) {
-      case MSGL_BF16: return dispatch_dim<bf16_t, fp8e4m3>(f, head_dim, group);
-      case MSGL_F16: return dispatch_dim<f16_t, fp8e4m3>(f, head_dim, group);
+      case MSGL_BF16: return decode_op_bf16_fp8(op, head_dim, group);
+      case MSGL_F16: return decode_op_f16_fp8(op, head_dim, group);
     }
     set_error("%s: fp8 pools take bf16 or fp16 queries (dtype %d)", fn, dtype);
     return MSGL_ERR_UNSUPPORTED;
   }
   switch (dtype) {
-    case MSGL_F32: return dispatch_dim<float>(f, head_dim, group);
-    case MSGL_BF16: return dispatch_dim<bf16_t>(f, head_dim, group);
-    case MSGL_F16: return dispatch_dim<f16_t>(f, head_dim, group);
+    case MSGL_F32: return decode_op_f32(op, head_dim, group);
+    case MSGL_BF16: return decode_op_bf16(op, head_dim, group);
+    case MSGL_F16: return decode_op_f16(op, head_dim, group);
   }
   set_error("%s: unknown dtype %d", fn, dtype);
   return MSGL_ERR_UNSUPPORTED;
+}
+
+// A launch request over p, and a query of the instantiation's properties.
+static DecodeOp launch_op(DecodeOpKind kind, const DecodeParams& p, int batch, hipStream_t stream) {
+  return DecodeOp{kind, &p, batch, stream, 0, nullptr, nullptr};
+}
+static DecodeOp query_op(DecodeOpKind kind, int nwaves, int* resident, bool* flag) {
+  return DecodeOp{kind, nullptr, 0, nullptr, nwaves, resident, flag};
 }
 
 // Workspace layout, each region 256-byte aligned: [meta | plan B*S*ngrp int4 |
@@ -722,7 +558,8 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
   p.hpg = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
   if (max_splits == 1) {
     bool shared = false;
-    const int st = dispatch(SharedOK{&shared}, dtype, kv_scale != nullptr, head_dim, num_qo_heads / num_kv_heads, fn);
+    const int st = dispatch(query_op(kOpShared, 0, nullptr, &shared), dtype, kv_scale != nullptr, head_dim,
+                            num_qo_heads / num_kv_heads, fn);
     if (st != MSGL_OK) return st;
     p.shared_head = shared;
   }
@@ -730,7 +567,7 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
     const int nwaves = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
     int resident = 0;
     bool ranges = false;
-    const int st = dispatch(Resident{nwaves, &resident, &ranges}, dtype, kv_scale != nullptr, head_dim,
+    const int st = dispatch(query_op(kOpResident, nwaves, &resident, &ranges), dtype, kv_scale != nullptr, head_dim,
                             num_qo_heads / num_kv_heads, fn);
     if (st != MSGL_OK) return st;
     p.balanced = ranges;
@@ -755,7 +592,7 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
                                     empty);
   if (st != MSGL_OK || empty) return st;
   p.skip_merge = (flags & MSGL_DECODE_NO_MERGE) != 0;
-  return dispatch(Launch{p, batch, (hipStream_t)stream}, dtype, kv_scale != nullptr, head_dim,
+  return dispatch(launch_op(kOpLaunch, p, batch, (hipStream_t)stream), dtype, kv_scale != nullptr, head_dim,
                   num_qo_heads / num_kv_heads, fn);
 }
 
@@ -827,12 +664,13 @@ extern "C" int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* 
   const int nwaves = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
   int resident = 0;
   bool ranges = false;
-  const int st = dispatch(Resident{nwaves, &resident, &ranges}, dtype, kv_fp8 != 0, head_dim,
+  const int st = dispatch(query_op(kOpResident, nwaves, &resident, &ranges), dtype, kv_fp8 != 0, head_dim,
                           num_qo_heads / num_kv_heads, "msgl_paged_decode_merge");
   if (st != MSGL_OK) return st;
   p.balanced = ranges;
   p.nranges = std::max(1, resident * MSGL_DECODE_RANGE_ROUNDS / p.ngrp);
-  return dispatch(MergeLaunch{p, batch, (hipStream_t)stream}, dtype, false, head_dim, num_qo_heads / num_kv_heads,
+  return dispatch(launch_op(kOpMerge, p, batch, (hipStream_t)stream), dtype, false, head_dim,
+                  num_qo_heads / num_kv_heads,
                   "msgl_paged_decode_merge");
 }
 

@@ -838,5 +838,19 @@ int prefill_params(const char* fn, int mode, const void* q, const void* k_pool, 
                    int32_t page_size, int64_t num_slots, int32_t dtype, float scale, int32_t max_splits, void* out,
                    void* workspace, int64_t workspace_bytes, PrefillParams& p, bool& empty);
 
+// The work-list launch of the 16-bit path, bq query tokens per block
+// (prefill.hip).
+int launch_prefill_plan(const PrefillParams& p, int bq, hipStream_t stream);
+
+// The launches of one (query, pool) type pair -- the work list unless p.mode
+// runs a stored one, the attention grid, the split-K merge -- for the
+// instantiation that head_dim and the query-head group select. Each is built in
+// a translation unit of its own (inst/prefill_*.hip over prefill_launch.h).
+int prefill_launch_f32(const PrefillParams& p, int max_e, int head_dim, int group, hipStream_t stream);
+int prefill_launch_bf16(const PrefillParams& p, int max_e, int head_dim, int group, hipStream_t stream);
+int prefill_launch_f16(const PrefillParams& p, int max_e, int head_dim, int group, hipStream_t stream);
+int prefill_launch_bf16_fp8(const PrefillParams& p, int max_e, int head_dim, int group, hipStream_t stream);
+int prefill_launch_f16_fp8(const PrefillParams& p, int max_e, int head_dim, int group, hipStream_t stream);
+
 }  // namespace pf
 }  // namespace msgl

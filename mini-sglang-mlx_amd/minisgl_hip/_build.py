@@ -42,11 +42,15 @@ COMMON_FLAGS = [
 
 
 def sources():
-    return sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")))
+    """csrc/*.hip, *.cpp and csrc/inst/*.hip (the kernel instantiations of one
+    (query, pool) type pair per file, so the largest units compile in parallel);
+    largest first, so the pool starts the longest compiles first."""
+    srcs = list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")) + list((CSRC / "inst").glob("*.hip"))
+    return sorted(srcs, key=lambda f: (f.parent.name != "inst", f.name))
 
 
 def _compile(src: Path, extra):
-    obj = BUILD / (src.name + ".o")
+    obj = BUILD / ("_".join(src.relative_to(CSRC).parts) + ".o")
     cmd = [HIPCC, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
