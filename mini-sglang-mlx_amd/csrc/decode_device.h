@@ -111,14 +111,15 @@ __device__ __forceinline__ int64_t balanced_range(int64_t ttot, int max_len, int
   return max(r, (int64_t)kMinChunk);
 }
 
-// A balanced launch is used when the ranges average at least this many keys:
-// shorter ranges measured slower on MI355X than per-request chunks (each chunk
-// pays its slot staging, fold and partial store, and the merge reads more
-// partials), longer ones faster (ragged long contexts leave no tail).
 // 0: no key-range form; split per request in chunks of one batch-wide length.
 #ifndef MSGL_DECODE_BALANCED
 #define MSGL_DECODE_BALANCED 1
 #endif
+
+// A balanced launch is used when the ranges average at least this many keys:
+// shorter ranges measured slower on MI355X than per-request chunks (each chunk
+// pays its slot staging, fold and partial store, and the merge reads more
+// partials), longer ones faster (ragged long contexts leave no tail).
 #ifndef MSGL_DECODE_BALANCED_MIN_RANGE
 #define MSGL_DECODE_BALANCED_MIN_RANGE 2048
 #endif
