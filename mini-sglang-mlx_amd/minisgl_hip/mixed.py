@@ -22,7 +22,12 @@ two work-list plans), plus one merge launch; with ``concurrent`` (and no single
 launch) the prefill runs on a second stream of default priority, forked after
 step 2 and joined before ``run`` returns. Either way the HBM-bound decode and
 the matrix-core-bound prefill share the GPU instead of running one after the
-other, and the results are bit-identical to running them in turn.
+other. The two-stream form runs the same launches as running the phases in
+turn, so its results are bit-identical to them. The single launch is
+bit-identical to them too while the decode phase splits requests into chunks.
+With one split the separate decode call runs its shared-head form, and for
+long-context batches it splits by equal key ranges; then the two agree to fp32
+rounding.
 """
 
 from __future__ import annotations

@@ -269,17 +269,19 @@ def mixed_case(
     dec_lo: int,
     dec_hi: int,
     prefill_prefixes,
-    chunk: int,
+    chunk,
     num_slots: int,
     page_size: int = 16,
     seed: int = 0,
 ) -> MixedCase:
     """num_decode decode requests with L ~ U_int[dec_lo, dec_hi], then one chunk of
-    ``chunk`` tokens over each prefix in ``prefill_prefixes``."""
+    ``chunk`` tokens over each prefix in ``prefill_prefixes`` (``chunk``: one
+    length for all, or one per prefix)."""
     rng = np.random.default_rng(seed)
     dec = rng.integers(dec_lo, dec_hi + 1, size=num_decode).astype(np.int64)
     pre = np.asarray(prefill_prefixes, dtype=np.int64)
-    device_len = np.concatenate([dec, pre + chunk]).astype(np.int32)
+    chunks = np.broadcast_to(np.asarray(chunk, dtype=np.int64), pre.shape)
+    device_len = np.concatenate([dec, pre + chunks]).astype(np.int32)
     cached_len = np.concatenate([dec - 1, pre]).astype(np.int32)
     r = len(device_len)
     num_pages = num_slots // page_size
