@@ -2,6 +2,8 @@
 // described at the top of mixed.hip). Included by the translation units under
 // inst/, each of which instantiates one query type, so the instantiations
 // compile in parallel.
+// The templates have internal linkage (anonymous namespace), like those of
+// decode_launch.h and prefill_launch.h.
 #pragma once
 
 #include "decode_device.h"

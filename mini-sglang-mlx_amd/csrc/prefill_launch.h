@@ -2,6 +2,10 @@
 // at the top of prefill.hip). Included by the translation units under inst/,
 // each of which instantiates one (query, pool) type pair, so the instantiations
 // compile in parallel.
+// The templates have internal linkage (anonymous namespace): a kernel that
+// several of those units instantiate -- the merge kernels, which do not depend
+// on the pool type -- gets its own copy and registration in each unit rather
+// than one external symbol registered by several code objects.
 #pragma once
 
 #include "prefill_device.h"
