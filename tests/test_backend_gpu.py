@@ -11,6 +11,7 @@ from gpu_util import assert_close, i32, randn, to_np64
 from minisgl_hip.attention import create_attention_backend
 from minisgl_hip.core import Batch, ModelConfig, Req
 from minisgl_hip.kvcache import MHAKVCache
+from test_kvquant_gpu import FP8, _codes, _deq
 
 pytestmark = pytest.mark.gpu
 
@@ -161,14 +162,20 @@ def test_fused_and_eager_store_agree(cuda_device):
     assert torch.equal(pools[0].view(torch.int16), pools[1].view(torch.int16))
 
 
-def test_mixed_batch_through_backend(cuda_device):
+@pytest.mark.parametrize("cache", ["bf16", "fp8", "f32"])
+def test_mixed_batch_through_backend(cuda_device, cache):
     """A continuous-batching step (4 decode requests, then a chunk over a cached
     prefix and a fresh prompt) as one batch of phase "mixed" through
-    prepare_metadata / store_kv / forward (msgl_mixed_attention), then a decode
-    step of all six: every request vs the oracle, new rows at out_loc."""
-    dt = torch.bfloat16
+    prepare_metadata / store_kv / forward, then a decode step of all six: every
+    request vs the oracle, new rows at out_loc. A bf16 cache takes the single
+    launch (msgl_mixed_attention). An fp8 cache runs the quantising fused decode,
+    then fp8 prefill: codes and scales at out_loc are bit-exact to the
+    quantiser, and the oracle reads the dequantised pool. An fp32 cache runs the
+    two phases in turn."""
+    fp8 = cache == "fp8"
+    dt = torch.float32 if cache == "f32" else torch.bfloat16
     cfg = ModelConfig(num_qo_heads=32, num_kv_heads=8, head_dim=128, num_layers=2)
-    kv = MHAKVCache(2, 16384, 8, 128, dt, cuda_device)
+    kv = MHAKVCache(2, 16384, 8, 128, dt, cuda_device, kv_dtype=FP8 if fp8 else None)
     table = np.zeros((10, 2048), dtype=np.int32)
     backend = create_attention_backend("hip", cfg, kv, table)
     free = np.random.default_rng(4).permutation(16384).astype(np.int32)
@@ -178,9 +185,15 @@ def test_mixed_batch_through_backend(cuda_device):
     reqs.append(Req(input_ids=np.zeros(300, np.int32), table_idx=7, cached_len=200))  # chunk over a cached prefix
     free = oracle.allocate_paged(table, free, [7], [0], [200], 1)
     reqs.append(Req(input_ids=np.zeros(77, np.int32), table_idx=9, cached_len=0))  # a fresh prompt
+    all_slots = torch.arange(16384, dtype=torch.int32, device=cuda_device)
     for layer in range(2):
-        kv.k[layer].copy_(randn(kv.k[layer].shape, 90 + layer, dt).to(cuda_device))
-        kv.v[layer].copy_(randn(kv.v[layer].shape, 95 + layer, dt).to(cuda_device))
+        k0 = randn(kv.k[layer].shape, 90 + layer, dt).to(cuda_device)
+        v0 = randn(kv.v[layer].shape, 95 + layer, dt).to(cuda_device)
+        if fp8:  # quantised rows in every slot
+            kv.store_kv(k0, v0, all_slots, layer)
+        else:
+            kv.k[layer].copy_(k0)
+            kv.v[layer].copy_(v0)
     for phase in ("mixed", "decode"):
         rows = [r.table_idx for r in reqs]
         cached = [r.cached_len for r in reqs]
@@ -200,18 +213,30 @@ def test_mixed_batch_through_backend(cuda_device):
             q = randn((t, 32, 128), 300 + layer, dt).to(cuda_device)
             k = randn((t, 8, 128), 310 + layer, dt).to(cuda_device)
             v = randn((t, 8, 128), 320 + layer, dt).to(cuda_device)
-            print(f"case backend {phase} layer={layer}", flush=True)
+            print(f"case backend {cache} {phase} layer={layer}", flush=True)
             kv.store_kv(k, v, batch.out_loc, layer)
             o = backend.forward(q, k, v, layer, batch)
             torch.cuda.synchronize()
             loc = batch.out_loc.long()
-            assert torch.equal(kv.k_cache(layer)[loc], k) and torch.equal(kv.v_cache(layer)[loc], v)
-            kp, vp = to_np64(kv.k[layer]), to_np64(kv.v[layer])
-            q_off, _, kvi = oracle.prefill_metadata(table, rows, cached, device)
-            # every request as a prefill of its extend rows over its whole context (a
-            # one-row extend attends like decode: attention/base.py:103, mask None)
-            ref = oracle.forward_prefill(to_np64(q), to_np64(k), to_np64(v), kp, vp, q_off, kvi, 128**-0.5)
-            assert_close(o, ref, dt, f"backend {phase} layer {layer}")
+            if fp8:
+                kc, ks = oracle.quantize_fp8(to_np64(k).astype(np.float32))
+                vc, vs = oracle.quantize_fp8(to_np64(v).astype(np.float32))
+                np.testing.assert_array_equal(_codes(kv.k_cache(layer))[out_loc], kc)
+                np.testing.assert_array_equal(_codes(kv.v_cache(layer))[out_loc], vc)
+                sc = kv.kv_scale[layer][loc].cpu().numpy()
+                np.testing.assert_array_equal(sc[..., 0], ks)
+                np.testing.assert_array_equal(sc[..., 1], vs)
+                kp, vp = _deq(kv.k[layer], kv.kv_scale[layer], 0), _deq(kv.v[layer], kv.kv_scale[layer], 1)
+            else:
+                assert torch.equal(kv.k_cache(layer)[loc], k) and torch.equal(kv.v_cache(layer)[loc], v)
+                kp, vp = to_np64(kv.k[layer]), to_np64(kv.v[layer])
+            q_off, _, _ = oracle.prefill_metadata(table, rows, cached, device)
+            # every request as a prefill of its extend rows over its whole context,
+            # read from the pool (a one-row extend attends like decode:
+            # attention/base.py:103, mask None)
+            kvi = [table[r, :n] for r, n in zip(rows, device)]
+            ref = oracle.forward_prefill(to_np64(q), None, None, kp, vp, q_off, kvi, 128**-0.5)
+            assert_close(o, ref, dt, f"backend {cache} {phase} layer {layer}")
         for r in reqs:
             if r.extend_len == 1 or phase == "mixed":
                 r.complete_one()
