@@ -781,7 +781,9 @@ def bench_mixed(args, dev):
 
 def bench_ceilings(args, dev):
     """The device's own ceilings next to the spec peaks: a 1 GiB device-to-device
-    copy (HBM read + write) and an 8192^3 bf16 GEMM (hipBLASLt via torch)."""
+    copy (HBM read + write), the same copy at the size of one fused RoPE + KV-store
+    launch (back to back, as that workload is timed) and an 8192^3 bf16 GEMM
+    (hipBLASLt via torch)."""
     import torch
 
     n = 1 << 30
@@ -798,6 +800,16 @@ def bench_ceilings(args, dev):
     sec, ev_s, _ = _timed(args, copy)
     copy_gbs = 2 * n / ev_s / 1e9
     del src, dst
+    # A copy the size of one fused RoPE + KV-store launch of the prefill chunk
+    # (33,439,936 bytes read + written), timed like that workload: 28 distinct
+    # buffer pairs back to back, median of steps -- the device-copy rate at that
+    # launch size.
+    small = 33439936 // 2
+    pairs = [(torch.empty(small, dtype=torch.uint8, device=dev), torch.empty(small, dtype=torch.uint8, device=dev))
+             for _ in range(LAYERS)]
+    small_s, _ = _b2b_step_time(args, lambda i: pairs[i][1].copy_(pairs[i][0]), LAYERS)
+    small_gbs = 2 * small * LAYERS / small_s / 1e9
+    del pairs
     m = 8192
     gen = torch.Generator(device=dev).manual_seed(0)
     a = torch.randn((m, m), generator=gen, device=dev, dtype=torch.bfloat16)
@@ -816,6 +828,7 @@ def bench_ceilings(args, dev):
         args, "device ceilings: copy GB/s and bf16 GEMM TFLOP/s", copy_gbs, "GB/s", sec * 1e3,
         "1 GiB device-to-device copy (read + write counted) and an 8192x8192x8192 bf16 GEMM (torch.matmul)",
         {"copy_gbs": round(copy_gbs, 1), "copy_frac_of_8tbs": round(copy_gbs / HBM_PEAK_GBS, 4),
+         "copy_33mb_b2b_us": round(small_s / LAYERS * 1e6, 2), "copy_33mb_b2b_gbs": round(small_gbs, 1),
          "gemm_tflops": round(tflops, 1), "gemm_frac_of_2500": round(tflops / MFMA_PEAK_TFLOPS, 4)},
         {"bound": "hbm", "achieved": round(copy_gbs, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
          "frac": round(copy_gbs / HBM_PEAK_GBS, 4), "traffic": 2 * n},

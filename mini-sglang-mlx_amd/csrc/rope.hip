@@ -24,8 +24,11 @@
 // loads and the cos/sin table is computed once into LDS, shared by all q and k
 // heads; rotation and stores follow. q is read and written, k and v read and
 // written once each. At a few thousand tokens the whole chunk is in flight at
-// once: the launch runs at ~3 TB/s (33 MB in ~11 µs), like a plain copy of
-// its size, rather than at the streaming rate.
+// once: the launch runs at ~3 TB/s (33 MB in ~11 µs), against ~4.2 TB/s for a
+// device copy of the same bytes timed the same way (28 launches back to back).
+// The slot order of the stores does not change the time, nor do 2 or 4 tokens
+// per workgroup: every token's loads land before its stores start, so the
+// chunk's reads and writes overlap little, where a copy streams both.
 #include "msgl_common.h"
 
 namespace msgl {
