@@ -49,8 +49,14 @@ def sources():
     return sorted(srcs, key=lambda f: (f.parent.name != "inst", f.name))
 
 
+def object_path(src: Path) -> Path:
+    """The object file of one source: its path under csrc/ joined by "_", so
+    csrc/inst/decode_bf16.hip and a csrc/decode_bf16.hip would not collide."""
+    return BUILD / ("_".join(src.relative_to(CSRC).parts) + ".o")
+
+
 def _compile(src: Path, extra):
-    obj = BUILD / ("_".join(src.relative_to(CSRC).parts) + ".o")
+    obj = object_path(src)
     cmd = [HIPCC, *COMMON_FLAGS, *extra, "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:

@@ -33,6 +33,21 @@ def test_every_declared_symbol_is_exported_and_bound():
     assert set(_lib.SIGNATURES) == names
 
 
+def test_build_compiles_every_source_to_its_own_object():
+    """The build's source list is every csrc/*.hip, csrc/*.cpp and
+    csrc/inst/*.hip, and no two sources share an object file (a shared name
+    would leave one unit's kernels out of the link)."""
+    from minisgl_hip import _build
+
+    srcs = _build.sources()
+    expected = (set(_build.CSRC.glob("*.hip")) | set(_build.CSRC.glob("*.cpp"))
+                | set((_build.CSRC / "inst").glob("*.hip")))
+    assert len(srcs) == len(expected) and set(srcs) == expected
+    assert any(s.parent.name == "inst" for s in srcs)
+    objs = [_build.object_path(s) for s in srcs]
+    assert len(set(objs)) == len(objs)
+
+
 def test_abi_version_and_sizes():
     lib = _lib.load()
     assert lib.msgl_abi_version() == 2
