@@ -125,6 +125,9 @@ int64_t msgl_paged_decode_workspace_size(int32_t batch, int32_t num_qo_heads, in
  *   workspace  >= msgl_paged_decode_workspace_size(B, Hq, Hkv, D, max_splits)
  *              bytes, 256-byte aligned
  * Launches the decode kernel and, when max_splits > 1, the split-K merge.
+ * Hq/Hkv 1 to 8, or a multiple of 8 (16 for Qwen3-235B-A22B's 64/4): a larger
+ * multiple runs as groups of 8 over Hq/8 virtual kv heads, the Hq/(8 Hkv) of
+ * one pool head reading its rows together; head_dim 64/128/256.
  * A request with L_b == 0 gets a zero output row. Memory-safe for any
  * metadata: index entries past kv_indptr[B] are not read and slots outside
  * [0, num_slots) read slot 0 (the result is then unspecified;

@@ -151,6 +151,10 @@ struct DecodeParams {
   int nranges;      // balanced split: key ranges of the launch (grid / ngrp)
   int64_t num_slots;
   int hq, hkv, page_size, max_splits, batch, ngrp;
+  // Query-head groups above 8 run as groups of 8 over hkv = hkv_pool * kv_rep
+  // virtual kv heads: virtual head v holds query heads [v G, v G + G) and reads
+  // pool head v / kv_rep. The pools, k_new and v_new have hkv_pool heads.
+  int hkv_pool, kv_rep;
   bool planned;   // the workspace already holds this call's plan
   bool balanced;  // equal key ranges of the batch's token stream allowed (else per-request chunks)
   bool shared_head;  // max_splits == 1: one (request, kv head) per 4-wavefront workgroup, tiles split over the waves
@@ -294,7 +298,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
   float* ML_lds = lds + 256 + 16;  // [16][2]
   uint8_t* K_lds = reinterpret_cast<uint8_t*>(lds + kLdsPerWave);  // [16][KRS bytes]
 
-  const int64_t row_stride = (int64_t)p.hkv * D * EKV;  // bytes per slot
+  const int64_t row_stride = (int64_t)p.hkv_pool * D * EKV;  // bytes per slot
   const int64_t nidx = p.kv_indptr[p.batch];             // entries of kv_indices
 
   // One chunk: keys [t0, t1) of request b (L keys, kv_indices from start),
@@ -344,8 +348,9 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
 #pragma unroll
       for (int e = 0; e < VKV; ++e) acc[g][e] = 0.f;
 
-    const uint8_t* kbase_p = reinterpret_cast<const uint8_t*>(p.k_pool) + (int64_t)kvh_c * D * EKV + vc * 16;
-    const uint8_t* vbase_p = reinterpret_cast<const uint8_t*>(p.v_pool) + (int64_t)kvh_c * D * EKV + vc * 16;
+    const int ph = kvh_c / p.kv_rep;  // the pool head this (virtual) kv head reads
+    const uint8_t* kbase_p = reinterpret_cast<const uint8_t*>(p.k_pool) + (int64_t)ph * D * EKV + vc * 16;
+    const uint8_t* vbase_p = reinterpret_cast<const uint8_t*>(p.v_pool) + (int64_t)ph * D * EKV + vc * 16;
 
     // Fused KV store (unquantised pools): the chunk holding position L-1 (the
     // new token) writes its rows to the pool and reads them from k_new/v_new
@@ -353,13 +358,14 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
     // inside the launch.
     const bool fused = !Q8 && p.k_new != nullptr;
     const int new_pos = fused && t1 == L ? L - 1 : 0x7fffffff;  // absolute position, or never
-    const int64_t new_off = ((int64_t)b * p.hkv + kvh_c) * D * ES + vc * VEC * ES;
+    const int64_t new_off = ((int64_t)b * p.hkv_pool + ph) * D * ES + vc * VEC * ES;
     const uint8_t* knew_p = fused ? reinterpret_cast<const uint8_t*>(p.k_new) + new_off : nullptr;
     const uint8_t* vnew_p = fused ? reinterpret_cast<const uint8_t*>(p.v_new) + new_off : nullptr;
-    if (active && new_pos != 0x7fffffff && lane < LPR && (!SHARED || wave == 0)) {
+    // (one virtual head of each pool head writes the row)
+    if (active && kvh_c % p.kv_rep == 0 && new_pos != 0x7fffffff && lane < LPR && (!SHARED || wave == 0)) {
       const int64_t slot = p.out_loc[b];
       if (slot >= 0 && slot < p.num_slots) {
-        const int64_t dst = slot * row_stride + (int64_t)kvh * D * ES + vc * VEC * ES;
+        const int64_t dst = slot * row_stride + (int64_t)ph * D * ES + vc * VEC * ES;
         st16(reinterpret_cast<uint8_t*>(p.k_pool_w) + dst, ld16(knew_p));
         st16(reinterpret_cast<uint8_t*>(p.v_pool_w) + dst, ld16(vnew_p));
       }

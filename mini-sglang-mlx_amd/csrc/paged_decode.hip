@@ -248,6 +248,27 @@ static inline int decode_groups(int hkv) {
   return (hkv + nwaves - 1) / nwaves;
 }
 
+// Query-head groups above 8 that are multiples of 8 run as groups of 8 over
+// virtual kv heads: virtual head v holds query heads 8v .. 8v+7 and reads pool
+// head v / rep (rep = G / 8). A workgroup's wavefronts hold neighbouring
+// virtual heads, so the rep wavefronts of one pool head read the same K/V rows
+// at about the same time and all but the first find them in L2, while the
+// group-8 kernel keeps its P.V accumulators in registers (a group of 16 needs
+// twice as many and spills). Every call maps its heads through this, so the
+// workspace, the plan, the decode and the merge agree; the map does not depend
+// on the pool type (the plan call does not know it), and fp8 pools, whose
+// scale staging is laid out by pool head, reject groups it maps (above 8).
+struct HeadMap {
+  int hkv;    // kv heads the kernels see
+  int group;  // query heads per such kv head
+  int rep;    // such kv heads per pool kv head
+};
+static inline HeadMap head_map(int hq, int hkv) {
+  const int g = hkv > 0 ? hq / hkv : 0;
+  if (g > 8 && g % 8 == 0) return HeadMap{hkv * (g / 8), 8, g / 8};
+  return HeadMap{hkv, g, 1};
+}
+
 struct DecodeWorkspace {
   int64_t plan, tok_off, part_ml, part_o, bytes;
 };
@@ -255,7 +276,7 @@ static inline DecodeWorkspace decode_workspace(int batch, int hq, int hkv, int h
   DecodeWorkspace w;
   const int64_t units = splits > 1 ? (int64_t)batch * splits * hq : 0;
   w.plan = 256;
-  w.tok_off = w.plan + align256((int64_t)batch * splits * decode_groups(hkv) * 16);
+  w.tok_off = w.plan + align256((int64_t)batch * splits * decode_groups(head_map(hq, hkv).hkv) * 16);
   w.part_ml = w.tok_off + align256(((int64_t)batch + 1) * 8);
   w.part_o = w.part_ml + align256(units * 2 * 4);
   w.bytes = w.part_o + align256(units * head_dim * 4);
@@ -359,11 +380,14 @@ extern "C" int msgl_paged_decode_plan(const int32_t* kv_indptr, const int32_t* s
   p.meta = reinterpret_cast<int*>(ws);
   p.plan = reinterpret_cast<int4*>(ws + w.plan);
   p.tok_off = reinterpret_cast<int64_t*>(ws + w.tok_off);
+  const HeadMap hm = head_map(num_qo_heads, num_kv_heads);
   p.hq = num_qo_heads;
-  p.hkv = num_kv_heads;
+  p.hkv = hm.hkv;
+  p.hkv_pool = num_kv_heads;
+  p.kv_rep = hm.rep;
   p.max_splits = max_splits;
   p.batch = batch;
-  p.ngrp = decode_groups(num_kv_heads);
+  p.ngrp = decode_groups(hm.hkv);
   hipLaunchKernelGGL(paged_decode_plan_kernel, dim3(1), dim3(kPlanThreads), 0, (hipStream_t)stream, p);
   MSGL_CHECK_LAUNCH("msgl_paged_decode_plan");
   return MSGL_OK;
@@ -542,12 +566,19 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
   p.tok_off = reinterpret_cast<int64_t*>(ws + w.tok_off);
   p.part_ml = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_ml) : nullptr;
   p.part_o = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_o) : nullptr;
+  const HeadMap hm = head_map(num_qo_heads, num_kv_heads);
+  if (kv_scale != nullptr && hm.rep > 1) {
+    set_error("%s: fp8 pools take Hq/Hkv 1 to 8 (got %d)", fn, num_qo_heads / num_kv_heads);
+    return MSGL_ERR_UNSUPPORTED;
+  }
   p.batch = batch;
-  p.ngrp = decode_groups(num_kv_heads);
+  p.ngrp = decode_groups(hm.hkv);
   p.planned = planned;
   p.num_slots = num_slots;
   p.hq = num_qo_heads;
-  p.hkv = num_kv_heads;
+  p.hkv = hm.hkv;
+  p.hkv_pool = num_kv_heads;
+  p.kv_rep = hm.rep;
   p.page_size = page_size;
   p.max_splits = max_splits;
   p.scale_log2 = scale * kLog2e;
@@ -555,20 +586,20 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
   p.skip_merge = false;
   p.nranges = 1;
   p.shared_head = false;
-  p.hpg = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
+  p.hpg = hm.hkv < MSGL_DECODE_WAVES_PER_WG ? hm.hkv : MSGL_DECODE_WAVES_PER_WG;
   if (max_splits == 1) {
     bool shared = false;
     const int st = dispatch(query_op(kOpShared, 0, nullptr, &shared), dtype, kv_scale != nullptr, head_dim,
-                            num_qo_heads / num_kv_heads, fn);
+                            hm.group, fn);
     if (st != MSGL_OK) return st;
     p.shared_head = shared;
   }
   if (max_splits > 1) {
-    const int nwaves = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
+    const int nwaves = hm.hkv < MSGL_DECODE_WAVES_PER_WG ? hm.hkv : MSGL_DECODE_WAVES_PER_WG;
     int resident = 0;
     bool ranges = false;
     const int st = dispatch(query_op(kOpResident, nwaves, &resident, &ranges), dtype, kv_scale != nullptr, head_dim,
-                            num_qo_heads / num_kv_heads, fn);
+                            hm.group, fn);
     if (st != MSGL_OK) return st;
     p.balanced = ranges;
     p.nranges = std::max(1, resident * MSGL_DECODE_RANGE_ROUNDS / p.ngrp);
@@ -593,7 +624,7 @@ static int paged_decode_impl(const char* fn, DecodeMode mode, const void* q, con
   if (st != MSGL_OK || empty) return st;
   p.skip_merge = (flags & MSGL_DECODE_NO_MERGE) != 0;
   return dispatch(launch_op(kOpLaunch, p, batch, (hipStream_t)stream), dtype, kv_scale != nullptr, head_dim,
-                  num_qo_heads / num_kv_heads, fn);
+                  p.hq / p.hkv, fn);
 }
 
 extern "C" int msgl_paged_decode_planned_ex(const void* q, const void* k_new, const void* v_new,
@@ -654,23 +685,30 @@ extern "C" int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* 
   p.tok_off = reinterpret_cast<int64_t*>(ws + w.tok_off);
   p.part_ml = reinterpret_cast<float*>(ws + w.part_ml);
   p.part_o = reinterpret_cast<float*>(ws + w.part_o);
+  const HeadMap hm = head_map(num_qo_heads, num_kv_heads);
+  if (kv_fp8 != 0 && hm.rep > 1) {
+    set_error("msgl_paged_decode_merge: fp8 pools take Hq/Hkv 1 to 8 (got %d)", num_qo_heads / num_kv_heads);
+    return MSGL_ERR_UNSUPPORTED;
+  }
   p.batch = batch;
   p.hq = num_qo_heads;
-  p.hkv = num_kv_heads;
+  p.hkv = hm.hkv;
+  p.hkv_pool = num_kv_heads;
+  p.kv_rep = hm.rep;
   p.max_splits = max_splits;
-  p.ngrp = decode_groups(num_kv_heads);
+  p.ngrp = decode_groups(hm.hkv);
   // the split form the decode launch chose: key ranges are sized by that
   // kernel's residency, so it is derived the way the decode call derives it
-  const int nwaves = num_kv_heads < MSGL_DECODE_WAVES_PER_WG ? num_kv_heads : MSGL_DECODE_WAVES_PER_WG;
+  const int nwaves = hm.hkv < MSGL_DECODE_WAVES_PER_WG ? hm.hkv : MSGL_DECODE_WAVES_PER_WG;
   int resident = 0;
   bool ranges = false;
   const int st = dispatch(query_op(kOpResident, nwaves, &resident, &ranges), dtype, kv_fp8 != 0, head_dim,
-                          num_qo_heads / num_kv_heads, "msgl_paged_decode_merge");
+                          hm.group, "msgl_paged_decode_merge");
   if (st != MSGL_OK) return st;
   p.balanced = ranges;
   p.nranges = std::max(1, resident * MSGL_DECODE_RANGE_ROUNDS / p.ngrp);
   return dispatch(launch_op(kOpMerge, p, batch, (hipStream_t)stream), dtype, false, head_dim,
-                  num_qo_heads / num_kv_heads,
+                  hm.group,
                   "msgl_paged_decode_merge");
 }
 

@@ -158,3 +158,93 @@ def test_mixed_groups(cuda_device, hq, hkv, d):
     if d == 128:
         for i in range(case.num_reqs):
             _check_request(case, i, q, kp, vp, b)
+
+
+# Query-head groups above 8 that are multiples of 8 run as groups of 8 over
+# virtual kv heads sharing their pool head's rows: Qwen3-235B-A22B (64 q / 4 kv,
+# G 16), G 16 at head_dim 64, and G 32 and 64.
+LARGE = [(64, 4, 128), (32, 2, 64), (32, 1, 256), (64, 2, 128), (64, 1, 64)]
+
+
+@pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
+@pytest.mark.parametrize("hq,hkv,d", LARGE)
+@pytest.mark.parametrize("splits", [1, None])
+def test_decode_large_groups(cuda_device, hq, hkv, d, dtype, splits):
+    """tests/test_attention.py:19-39's batch (lens [1,2,17,31,32,33,700], N=4096)."""
+    dt = DTYPES[dtype]
+    c = workloads.reference_test_case()
+    kp = randn((4096, hkv, d), 350, dt).to(cuda_device)
+    vp = randn((4096, hkv, d), 351, dt).to(cuda_device)
+    q = randn((7, hq, d), 352, dt).to(cuda_device)
+    print(f"case decode large groups {hq}/{hkv}/{d} {dtype} splits={splits}", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device),
+                                     d**-0.5, max_splits=splits)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(to_np64(q), to_np64(kp), to_np64(vp), c.kv_indptr, c.kv_indices, d**-0.5)
+    assert_close(out, ref, dt, f"decode large groups {hq}/{hkv}/{d} {dtype} splits={splits}")
+
+
+@pytest.mark.parametrize("hq,hkv,d", LARGE)
+def test_decode_large_groups_store_plan_merge(cuda_device, hq, hkv, d):
+    """Bit for bit (bf16, lengths across tiles, page 16): the fused store + decode
+    equals the store then the decode (the pools included), a plan built once
+    equals the self-planning call, and the decode launch without its merge
+    followed by the separate merge equals the call with it."""
+    dt = torch.bfloat16
+    lens = [1, 2, 17, 64, 65, 300, 1000, 2500]
+    c = workloads.decode_case_from_lens(lens, num_slots=8192, page_size=16, seed=29)
+    kp = randn((8192, hkv, d), 360, dt).to(cuda_device)
+    vp = randn((8192, hkv, d), 361, dt).to(cuda_device)
+    q = randn((len(lens), hq, d), 362, dt).to(cuda_device)
+    kn = randn((len(lens), hkv, d), 363, dt).to(cuda_device)
+    vn = randn((len(lens), hkv, d), 364, dt).to(cuda_device)
+    loc = i32(c.out_loc, cuda_device)
+    indptr, pages, sl = i32(c.page_indptr, cuda_device), i32(c.page_ids, cuda_device), i32(c.lens, cuda_device)
+    kw = dict(seq_lens=sl, page_size=16, max_splits=4)
+    kp2, vp2 = kp.clone(), vp.clone()
+    print(f"case decode large groups store/plan/merge {hq}/{hkv}/{d}", flush=True)
+    fused = ops.paged_decode_attention(q, kp, vp, indptr, pages, d**-0.5, new_kv=(kn, vn, loc), **kw)
+    ops.store_kv(kn, vn, loc, kp2, vp2)
+    two = ops.paged_decode_attention(q, kp2, vp2, indptr, pages, d**-0.5, **kw)
+    ws = ops.decode_workspace(len(lens), hq, hkv, d, 4, cuda_device)
+    ops.paged_decode_plan(indptr, sl, len(lens), hq, hkv, d, 4, ws)
+    planned = ops.paged_decode_attention(q, kp2, vp2, indptr, pages, d**-0.5, workspace=ws, planned=True, **kw)
+    apart = ops.paged_decode_attention(q, kp2, vp2, indptr, pages, d**-0.5, workspace=ws, planned=True, merge=False,
+                                       **kw)
+    ops.paged_decode_merge(apart, indptr, sl, hkv, 4, ws)
+    torch.cuda.synchronize()
+    assert torch.equal(kp.view(torch.int16), kp2.view(torch.int16))
+    assert torch.equal(vp.view(torch.int16), vp2.view(torch.int16))
+    assert torch.equal(fused, two) and torch.equal(planned, two) and torch.equal(apart, two)
+    ref = oracle.paged_decode(to_np64(q), to_np64(kp2), to_np64(vp2), c.kv_indptr, c.kv_indices, d**-0.5)
+    assert_close(fused, ref, dt, f"fused decode large groups {hq}/{hkv}/{d}")
+
+
+def test_decode_large_group_long_contexts(cuda_device):
+    """Qwen3-235B-A22B heads (64 q / 4 kv, head_dim 128, bf16) over about a
+    million keys, long enough for equal key ranges: sampled requests vs the
+    oracle, and the fused store bit for bit."""
+    dt = torch.bfloat16
+    hq, hkv, d = 64, 4, 128
+    lens = np.random.default_rng(31).integers(6000, 14000, 96)
+    n = int(lens.sum()) + 8192
+    c = workloads.decode_case_from_lens(lens, num_slots=n, seed=31)
+    g = torch.Generator(device=cuda_device).manual_seed(370)  # 1 GB pools: drawn on the device
+    kp = torch.randn((n, hkv, d), generator=g, device=cuda_device).to(dt)
+    vp = torch.randn((n, hkv, d), generator=g, device=cuda_device).to(dt)
+    q = randn((len(lens), hq, d), 372, dt).to(cuda_device)
+    kn = randn((len(lens), hkv, d), 373, dt).to(cuda_device)
+    vn = randn((len(lens), hkv, d), 374, dt).to(cuda_device)
+    loc = i32(c.out_loc, cuda_device)
+    print(f"case decode large group long contexts keys={int(lens.sum())}", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device),
+                                     d**-0.5, new_kv=(kn, vn, loc))
+    torch.cuda.synchronize()
+    lo = loc.long()
+    assert torch.equal(kp[lo], kn) and torch.equal(vp[lo], vn)
+    for b in (0, 17, 50, 95):
+        idx = c.kv_indices[c.kv_indptr[b]: c.kv_indptr[b + 1]]
+        sel = torch.from_numpy(idx.astype(np.int64)).to(cuda_device)
+        ref = oracle.paged_decode(to_np64(q[b: b + 1]), to_np64(kp[sel]), to_np64(vp[sel]),
+                                  np.array([0, len(idx)]), np.arange(len(idx)), d**-0.5)
+        assert_close(out[b: b + 1], ref, dt, f"decode large group long contexts request {b}")
