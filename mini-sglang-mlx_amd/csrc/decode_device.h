@@ -180,6 +180,11 @@ __device__ __forceinline__ bool balanced_launch(const DecodeParams& p) {
          p.tok_off[p.batch] >= (int64_t)MSGL_DECODE_BALANCED_MIN_RANGE * p.nranges;
 }
 
+// Lazy online softmax: a row's reference maximum moves only when a tile's
+// maximum exceeds it by more than 2^kLazyLog2, so most tiles skip the rescale
+// of the G x (16 / sizeof T) accumulators.
+constexpr float kLazyLog2 = 8.f;
+
 // LDS per wavefront: P tile [16 tokens][16 rows] + alpha[16] + (m, l)[16 rows].
 constexpr int kLdsPerWave = 16 * 16 + 16 + 32;
 
@@ -499,12 +504,18 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
         const float sc = Q8 ? p.scale_log2 * ks : p.scale_log2;
         const bool valid = tile * 16 + r < seg_len;
         float pr[4] = {0.f, 0.f, 0.f, 0.f}, al[4] = {1.f, 1.f, 1.f, 1.f};
+        bool moved = false;  // some row's reference maximum moved (its accumulators need al)
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
           const float x = valid ? s[i] * sc : -INFINITY;
-          const float mt = row16_max(x);
-          const float m_new = fmaxf(m_run[i], mt);
-          al[i] = __builtin_amdgcn_exp2f(m_run[i] - m_new);
+          const float mt = row16_max(x);  // finite: key 0 of every tile is valid
+          // the reference maximum moves only when the tile's exceeds it by more
+          // than 2^kLazyLog2 (a weight stays below 2^kLazyLog2; l and O share the
+          // reference, so the result is the same up to rounding)
+          const bool mv = mt > m_run[i] + kLazyLog2;
+          const float m_new = mv ? mt : m_run[i];
+          al[i] = mv ? __builtin_amdgcn_exp2f(m_run[i] - m_new) : 1.f;
+          moved |= mv;
           pr[i] = __builtin_amdgcn_exp2f(x - m_new);
           l_run[i] = l_run[i] * al[i] + pr[i];
           m_run[i] = m_new;
@@ -515,14 +526,16 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
         *reinterpret_cast<f32x4*>(P_lds + r * 16 + 4 * g4) = f32x4{pr[0] * vsc, pr[1] * vsc, pr[2] * vsc, pr[3] * vsc};
         if (r == 0) *reinterpret_cast<f32x4*>(A_lds + 4 * g4) = f32x4{al[0], al[1], al[2], al[3]};
         wave_lds_sync();
-        // O = alpha * O + P V on the VALU
-        float alpha[G];
+        // O = alpha * O + P V on the VALU (alpha only when a row's reference moved)
+        if (__builtin_amdgcn_ballot_w64(moved) != 0) {
+          float alpha[G];
 #pragma unroll
-        for (int g = 0; g < G; ++g) alpha[g] = A_lds[g];
+          for (int g = 0; g < G; ++g) alpha[g] = A_lds[g];
 #pragma unroll
-        for (int g = 0; g < G; ++g)
+          for (int g = 0; g < G; ++g)
 #pragma unroll
-          for (int e = 0; e < VKV; ++e) acc[g][e] *= alpha[g];
+            for (int e = 0; e < VKV; ++e) acc[g][e] *= alpha[g];
+        }
 #pragma unroll
         for (int i = 0; i < NLV; ++i) {
           const int tl = vr + R * i;

@@ -41,7 +41,9 @@
 //    faster than one spanning 16 rows x 64 B (the B layout's own shape).
 //  * Online softmax in the exp2 domain (scale*log2(e) folded into the score)
 //    with the tile max over 16 tokens from 4 DPP steps inside a 16-lane row;
-//    only the MFMA rows that hold query heads are processed.
+//    only the MFMA rows that hold query heads are processed. The reference
+//    maximum moves lazily (only when a tile's exceeds it by 2^8), so most
+//    tiles skip the accumulators' rescale.
 //  * P.V on the VALU: lane (token sub-row, 16-byte d chunk) accumulates
 //    G x (16/sizeof T) fp32 outputs; P and the rescale factors go through a
 //    small per-wave LDS tile.
