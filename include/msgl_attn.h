@@ -375,7 +375,8 @@ int msgl_store_kv_fp8(const void* k, const void* v, const int32_t* out_loc, void
  * msgl_paged_decode over fp8 pools (attention/metal.py:112-131 semantics over
  * the dequantised pool): scores use e4m3(code) on the matrix core with the
  * row's K scale applied to the score, the V scale folds into the softmax
- * weight. q/out dtype bf16 or fp16; Hq/Hkv from 1 to 8; head_dim 64/128/256.
+ * weight. q/out dtype bf16 or fp16; Hq/Hkv 1 to 8 or a multiple of 8 (as
+ * msgl_paged_decode); head_dim 64/128/256.
  * Same workspace (msgl_paged_decode_workspace_size) and plan
  * (msgl_paged_decode_plan) as the unquantised decode; the _planned form skips
  * the plan like msgl_paged_decode_planned. The new token is stored first with

@@ -379,7 +379,9 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
     // K and V rows exactly like msgl_store_kv_fp8 (lanes [0, LQ) the K row,
     // [LQ, 2 LQ) the V row, one 16-byte chunk of T each) and writes codes and
     // scales before any load of the chunk is issued; the loop then reads the
-    // new token from the pool like every other token.
+    // new token from the pool like every other token. Every virtual head of a
+    // pool head writes the same bytes, and each reads back only after its own
+    // writes have landed, so none reads a slot half written.
     if constexpr (Q8) {
       if (active && p.k_new != nullptr && t1 == L) {
         constexpr int LQ = D / VEC;  // lanes per input row
@@ -387,16 +389,16 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
         const int sub = lane % LQ;
         const bool is_v = (lane / LQ) & 1;  // lanes >= 2 LQ repeat the rows and write nothing
         const uint8_t* src = reinterpret_cast<const uint8_t*>(is_v ? p.v_new : p.k_new) +
-                             (((int64_t)b * p.hkv + kvh) * D + sub * VEC) * ES;
+                             (((int64_t)b * p.hkv_pool + ph) * D + sub * VEC) * ES;
         uint32_t w[VEC / 4];
         const float amax = fp8_quantize_chunk<T>(ld16(src), LQ, w);
         const int64_t slot = p.out_loc[b];
         if (lane < 2 * LQ && slot >= 0 && slot < p.num_slots) {
           uint8_t* dst = reinterpret_cast<uint8_t*>(is_v ? p.v_pool_w : p.k_pool_w) +
-                         (slot * p.hkv + kvh) * D + sub * VEC;
+                         (slot * p.hkv_pool + ph) * D + sub * VEC;
           static_assert(VEC == 8, "16-bit queries: eight codes per lane");
           *reinterpret_cast<uint2*>(dst) = make_uint2(w[0], w[1]);
-          if (sub == 0) p.kv_scale_w[(slot * p.hkv + kvh) * 2 + (is_v ? 1 : 0)] = amax / 448.f;
+          if (sub == 0) p.kv_scale_w[(slot * p.hkv_pool + ph) * 2 + (is_v ? 1 : 0)] = amax / 448.f;
         }
         // the stores have completed before this wavefront loads the slot back
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
@@ -426,7 +428,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
         const int total = (ntile + NST - 1) * 16 * nd;
         const int h0 = kgrp * nwaves;
         const uint32_t sbase = (uint32_t)(uintptr_t)((MSGL_LDS float*)scale_lds);
-        if (nwaves == 4 && (p.hkv & 3) == 0) {
+        if (nwaves == 4 && (p.hkv & 3) == 0 && p.kv_rep == 1) {
           // four heads, all present: a token's 32 bytes are two aligned 16-byte transfers
           const int total16 = total >> 2;
           for (int c = wave; c * 64 < total16; c += nwaves) {
@@ -441,7 +443,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
             if (idx < total) {
               const int t = idx / nd, d = idx - t * nd;
               const int h = min(h0 + (d >> 1), p.hkv - 1);  // heads past hkv: an inactive wave's, never read
-              dma4(p.kv_scale + ((int64_t)slots_lds[t] * p.hkv + h) * 2 + (d & 1),
+              dma4(p.kv_scale + ((int64_t)slots_lds[t] * p.hkv_pool + h / p.kv_rep) * 2 + (d & 1),
                    __builtin_amdgcn_readfirstlane(sbase + c * 256));
             }
           }
@@ -470,7 +472,7 @@ __device__ __forceinline__ void paged_decode_body(const DecodeParams& p, int wg)
           buf.v[i] = ld16_stream(is_new ? vnew_p : vbase_p + off);
         }
         if (Q8 && !SCL) {  // the K and V scales of the token in this lane's MFMA column: one 8-byte load
-          const float2 sc = reinterpret_cast<const float2*>(p.kv_scale)[(int64_t)slots_lds[base + r] * p.hkv + kvh_c];
+          const float2 sc = reinterpret_cast<const float2*>(p.kv_scale)[(int64_t)slots_lds[base + r] * p.hkv_pool + ph];
           buf.ks = sc.x;
           buf.vs = sc.y;
         }

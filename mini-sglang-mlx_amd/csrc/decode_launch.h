@@ -71,7 +71,8 @@ int launch_decode(const DecodeParams& p_in, int batch, hipStream_t stream) {
         // fp8 pools: the quantising store first (the waves of a workgroup do not
         // read back a slot another of them wrote), then the decode reads it
         const int st = msgl_store_kv_fp8(p.k_new, p.v_new, p.out_loc, p.k_pool_w, p.v_pool_w, p.kv_scale_w, batch,
-                                         p.hkv, D, p.num_slots, std::is_same<T, bf16_t>::value ? MSGL_BF16 : MSGL_F16,
+                                         p.hkv_pool, D, p.num_slots,
+                                         std::is_same<T, bf16_t>::value ? MSGL_BF16 : MSGL_F16,
                                          stream);
         if (st != MSGL_OK) return st;
         p.k_new = p.v_new = nullptr;

@@ -258,8 +258,8 @@ static inline int decode_groups(int hkv) {
 // group-8 kernel keeps its P.V accumulators in registers (a group of 16 needs
 // twice as many and spills). Every call maps its heads through this, so the
 // workspace, the plan, the decode and the merge agree; the map does not depend
-// on the pool type (the plan call does not know it), and fp8 pools, whose
-// scale staging is laid out by pool head, reject groups it maps (above 8).
+// on the pool type (the plan call does not know it). fp8 pools read their
+// scales by pool head too.
 struct HeadMap {
   int hkv;    // kv heads the kernels see
   int group;  // query heads per such kv head
@@ -569,10 +569,6 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
   p.part_ml = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_ml) : nullptr;
   p.part_o = max_splits > 1 ? reinterpret_cast<float*>(ws + w.part_o) : nullptr;
   const HeadMap hm = head_map(num_qo_heads, num_kv_heads);
-  if (kv_scale != nullptr && hm.rep > 1) {
-    set_error("%s: fp8 pools take Hq/Hkv 1 to 8 (got %d)", fn, num_qo_heads / num_kv_heads);
-    return MSGL_ERR_UNSUPPORTED;
-  }
   p.batch = batch;
   p.ngrp = decode_groups(hm.hkv);
   p.planned = planned;
@@ -688,10 +684,6 @@ extern "C" int msgl_paged_decode_merge(const int32_t* kv_indptr, const int32_t* 
   p.part_ml = reinterpret_cast<float*>(ws + w.part_ml);
   p.part_o = reinterpret_cast<float*>(ws + w.part_o);
   const HeadMap hm = head_map(num_qo_heads, num_kv_heads);
-  if (kv_fp8 != 0 && hm.rep > 1) {
-    set_error("msgl_paged_decode_merge: fp8 pools take Hq/Hkv 1 to 8 (got %d)", num_qo_heads / num_kv_heads);
-    return MSGL_ERR_UNSUPPORTED;
-  }
   p.batch = batch;
   p.hq = num_qo_heads;
   p.hkv = hm.hkv;

@@ -181,7 +181,7 @@ def test_host_side_argument_errors():
         16, 16, 16, sc, 16, 16, nul, 4, hq, 8, d, 1, 100, dtype, 0.1, 1, 16, 256, 1 << 30, nul)
     assert df(sc=nul) == _lib.MSGL_ERR_INVALID and "kv_scale" in _lib.last_error()
     assert df(dtype=0) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()  # fp32 q over fp8 pools
-    assert df(hq=128) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()  # group 16
+    assert df(hq=96) == _lib.MSGL_ERR_UNSUPPORTED and "fp8" in _lib.last_error()  # group 12: not built
     assert df(d=96) == _lib.MSGL_ERR_UNSUPPORTED and "head_dim" in _lib.last_error()
     assert df(sc=12) == _lib.MSGL_ERR_INVALID and "aligned" in _lib.last_error()
     # fp8 decode with the fused store: (q, k_new, v_new, out_loc, kp, vp, kv_scale, indptr, ...)

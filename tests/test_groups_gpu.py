@@ -248,3 +248,44 @@ def test_decode_large_group_long_contexts(cuda_device):
         ref = oracle.paged_decode(to_np64(q[b: b + 1]), to_np64(kp[sel]), to_np64(vp[sel]),
                                   np.array([0, len(idx)]), np.arange(len(idx)), d**-0.5)
         assert_close(out[b: b + 1], ref, dt, f"decode large group long contexts request {b}")
+
+
+@pytest.mark.parametrize("hq,hkv,d", [(64, 4, 128), (32, 2, 64), (64, 1, 64)])
+@pytest.mark.parametrize("splits", [1, 4])
+def test_fp8_decode_large_groups(cuda_device, hq, hkv, d, splits):
+    """fp8 pools with groups of 16 and 64 (virtual kv heads reading their pool
+    head's codes and scales): decode over the reference batch against the
+    oracle on the dequantised pool, and the fused quantising store + decode
+    equal to msgl_store_kv_fp8 then the decode, codes, scales and output bit for
+    bit (lengths across tiles, key-range chunks)."""
+    dt = torch.bfloat16
+    c = workloads.reference_test_case()
+    kp, vp, sc, _, _ = _fp8_pools(4096, hkv, d, 380, cuda_device)
+    q = randn((7, hq, d), 382, dt).to(cuda_device)
+    print(f"case fp8 large groups {hq}/{hkv}/{d} splits={splits}", flush=True)
+    out = ops.paged_decode_attention(q, kp, vp, i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device),
+                                     d**-0.5, max_splits=splits, kv_scale=sc)
+    torch.cuda.synchronize()
+    ref = oracle.paged_decode(to_np64(q), _deq(kp, sc, 0), _deq(vp, sc, 1), c.kv_indptr, c.kv_indices, d**-0.5)
+    assert_close(out, ref, dt, f"fp8 decode large groups {hq}/{hkv}/{d} splits={splits}")
+
+    lens = [1, 2, 17, 64, 65, 300, 1000, 2500]
+    c = workloads.decode_case_from_lens(lens, num_slots=8192, seed=37)
+    kp, vp, sc, _, _ = _fp8_pools(8192, hkv, d, 390, cuda_device)
+    q = randn((len(lens), hq, d), 392, dt).to(cuda_device)
+    kn = randn((len(lens), hkv, d), 393, dt).to(cuda_device)
+    vn = randn((len(lens), hkv, d), 394, dt).to(cuda_device)
+    loc = i32(c.out_loc, cuda_device)
+    indptr, indices = i32(c.kv_indptr, cuda_device), i32(c.kv_indices, cuda_device)
+    kp2, vp2, sc2 = kp.clone(), vp.clone(), sc.clone()
+    fused = ops.paged_decode_attention(q, kp, vp, indptr, indices, d**-0.5, max_splits=splits, kv_scale=sc,
+                                       new_kv=(kn, vn, loc))
+    ops.store_kv_fp8(kn, vn, loc, kp2, vp2, sc2)
+    two = ops.paged_decode_attention(q, kp2, vp2, indptr, indices, d**-0.5, max_splits=splits, kv_scale=sc2)
+    torch.cuda.synchronize()
+    assert torch.equal(kp.view(torch.uint8), kp2.view(torch.uint8))
+    assert torch.equal(vp.view(torch.uint8), vp2.view(torch.uint8))
+    assert torch.equal(sc, sc2)
+    assert torch.equal(fused, two)
+    ref = oracle.paged_decode(to_np64(q), _deq(kp2, sc2, 0), _deq(vp2, sc2, 1), c.kv_indptr, c.kv_indices, d**-0.5)
+    assert_close(fused, ref, dt, f"fp8 fused decode large groups {hq}/{hkv}/{d} splits={splits}")
