@@ -256,7 +256,9 @@ static inline int decode_groups(int hkv) {
 // virtual heads, so the rep wavefronts of one pool head read the same K/V rows
 // at about the same time and all but the first find them in L2, while the
 // group-8 kernel keeps its P.V accumulators in registers (a group of 16 needs
-// twice as many and spills). Every call maps its heads through this, so the
+// twice as many and spills). A group of 8 over one or two pool heads runs as
+// groups of 4 over twice the heads: more wavefronts per token where there are
+// few (measured faster with the default split bound). Every call maps its heads through this, so the
 // workspace, the plan, the decode and the merge agree; the map does not depend
 // on the pool type (the plan call does not know it). fp8 pools read their
 // scales by pool head too.
@@ -268,6 +270,7 @@ struct HeadMap {
 static inline HeadMap head_map(int hq, int hkv) {
   const int g = hkv > 0 ? hq / hkv : 0;
   if (g > 8 && g % 8 == 0) return HeadMap{hkv * (g / 8), 8, g / 8};
+  if (g == 8 && hkv <= 2) return HeadMap{hkv * 2, 4, 2};
   return HeadMap{hkv, g, 1};
 }
 
@@ -293,6 +296,8 @@ static inline DecodeWorkspace decode_workspace(int batch, int hq, int hkv, int h
 
 
 }  // namespace msgl
+
+int msgl::dec::decode_kv_rep(int hq, int hkv) { return head_map(hq, hkv).rep; }
 
 int64_t msgl::dec::decode_items(const DecodeParams& p) {
   // a balanced launch is chosen on the device (balanced_launch), so the grid

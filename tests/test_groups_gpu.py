@@ -131,7 +131,8 @@ def test_fp8_groups(cuda_device, hq, hkv, d, splits):
     assert_close(out, _fp8_prefill_oracle(case, q, kp, vp, sc, d), dt, f"fp8 prefill groups {hq}/{hkv}/{d}")
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(24, 8, 128), (40, 8, 128), (28, 4, 128), (14, 2, 64), (32, 2, 128)])
+@pytest.mark.parametrize("hq,hkv,d", [(24, 8, 128), (40, 8, 128), (28, 4, 128), (14, 2, 64), (32, 2, 128),
+                                     (16, 2, 128)])
 def test_mixed_groups(cuda_device, hq, hkv, d):
     """msgl_mixed_attention: bit-identical to the decode and prefill calls run in
     turn; every request against the oracle (head_dim 128)."""
@@ -160,10 +161,11 @@ def test_mixed_groups(cuda_device, hq, hkv, d):
             _check_request(case, i, q, kp, vp, b)
 
 
-# Query-head groups above 8 that are multiples of 8 run as groups of 8 over
-# virtual kv heads sharing their pool head's rows: Qwen3-235B-A22B (64 q / 4 kv,
-# G 16), G 16 at head_dim 64, and G 32 and 64.
-LARGE = [(64, 4, 128), (32, 2, 64), (32, 1, 256), (64, 2, 128), (64, 1, 64)]
+# Layouts the decode runs over virtual kv heads sharing their pool head's rows:
+# groups above 8 that are multiples of 8 as groups of 8 (Qwen3-235B-A22B's 64 q
+# / 4 kv, G 16 at head_dim 64, G 32 and 64), and groups of 8 over one or two
+# pool heads as groups of 4 over twice the heads (Qwen2.5-3B's 16 / 2, 8 / 1).
+LARGE = [(64, 4, 128), (32, 2, 64), (32, 1, 256), (64, 2, 128), (64, 1, 64), (16, 2, 128), (8, 1, 64)]
 
 
 @pytest.mark.parametrize("dtype", ["f32", "bf16", "f16"])
@@ -250,10 +252,10 @@ def test_decode_large_group_long_contexts(cuda_device):
         assert_close(out[b: b + 1], ref, dt, f"decode large group long contexts request {b}")
 
 
-@pytest.mark.parametrize("hq,hkv,d", [(64, 4, 128), (32, 2, 64), (64, 1, 64)])
+@pytest.mark.parametrize("hq,hkv,d", [(64, 4, 128), (32, 2, 64), (64, 1, 64), (16, 2, 128)])
 @pytest.mark.parametrize("splits", [1, 4])
 def test_fp8_decode_large_groups(cuda_device, hq, hkv, d, splits):
-    """fp8 pools with groups of 16 and 64 (virtual kv heads reading their pool
+    """fp8 pools with groups of 16, 64 and 8 over two heads (virtual kv heads reading their pool
     head's codes and scales): decode over the reference batch against the
     oracle on the dequantised pool, and the fused quantising store + decode
     equal to msgl_store_kv_fp8 then the decode, codes, scales and output bit for
