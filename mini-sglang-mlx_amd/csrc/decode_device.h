@@ -875,10 +875,6 @@ int64_t decode_items(const DecodeParams& p);
 // The work-list launch (paged_decode.hip).
 int launch_decode_plan(const DecodeParams& p, hipStream_t stream);
 
-// Virtual kv heads per pool kv head that the decode runs Hq/Hkv as (1: the
-// pool's heads themselves). (paged_decode.hip)
-int decode_kv_rep(int hq, int hkv);
-
 // A request to the instantiation that (query type, pool type, head_dim, query-
 // head group) selects: the decode launch (plan unless p->planned, attention,
 // merge), the merge launch alone, or a property of the instantiation.

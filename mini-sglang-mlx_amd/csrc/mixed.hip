@@ -60,13 +60,13 @@ extern "C" int msgl_mixed_attention(const void* q_dec, const void* k_new, const 
   MSGL_CHECK_ARG(num_decode >= 0 && num_prefill >= 0, "msgl_mixed_attention: request counts must be >= 0");
   // The single launch is built for 16-bit q, head_dim 64 and 128 and Hq/Hkv 1
   // to 8 (a larger group's decode accumulators do not fit beside the prefill
-  // body's registers) where the decode runs the pool's own kv heads (its one
-  // group serves both bodies). Other shapes, and batches of one phase, run the phases
+  // body's registers); its decode body takes the decode's group (4 where the
+  // decode runs 8 over virtual kv heads). Other shapes, and batches of one phase, run the phases
   // as launches of their own on the stream: the same results as the decode and
   // prefill calls, which touch disjoint slots (a request is in one phase).
   const int group = num_kv_heads > 0 && num_qo_heads % num_kv_heads == 0 ? num_qo_heads / num_kv_heads : 0;
   const bool one_launch = (dtype == MSGL_BF16 || dtype == MSGL_F16) && (head_dim == 64 || head_dim == 128) &&
-                          group >= 1 && group <= 8 && dec::decode_kv_rep(num_qo_heads, num_kv_heads) == 1;
+                          group >= 1 && group <= 8;
   if (num_decode == 0 || num_prefill == 0 || max_extend_len == 0 || num_tokens == 0 || !one_launch) {
     int st = MSGL_OK;
     if (num_prefill > 0)

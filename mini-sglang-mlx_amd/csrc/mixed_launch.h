@@ -24,7 +24,10 @@ int mixed_launch_f16(const pf::PrefillParams& pp, const dec::DecodeParams& dp, i
 namespace msgl {
 namespace {
 
-template <typename T, int D, int G>
+// G: query heads per kv head of the prefill body; GD: of the decode body, which
+// runs the decode's kv heads (virtual ones where it maps G 8 over Hkv <= 2 to
+// groups of 4).
+template <typename T, int D, int G, int GD>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf::G16<D>::WAVES))) void mixed_attention_kernel(
     pf::PrefillParams pp, dec::DecodeParams dp) {
   const int np = *pp.plan_count;
@@ -40,24 +43,24 @@ __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(pf::G16<D>:
     if (item < np) pf::prefill16_body<T, T, D, G>(pp, item);
   } else {
     const int item = 8 * (c - a) + j;
-    if (item < nd) dec::paged_decode_body<T, T, D, G, false>(dp, item);
+    if (item < nd) dec::paged_decode_body<T, T, D, GD, false>(dp, item);
   }
 }
 
 // The split-K merges of both parts: the first npm workgroups are the prefill
 // merge's (token tk = i % ntok, head block i / ntok), the rest the decode merge's.
-template <typename T, int D, int G>
+template <typename T, int D, int GD>
 __global__ __launch_bounds__(256) void mixed_merge_kernel(pf::PrefillParams pp, dec::DecodeParams dp, int batch,
                                                           int ntok, int npm) {
   const int i = blockIdx.x;
   if (i < npm) {
     pf::prefill_merge_body<T, D>(pp, i % ntok, i / ntok);
   } else {
-    dec::paged_decode_merge_body<T, D, G>(dp, batch, i - npm);
+    dec::paged_decode_merge_body<T, D, GD>(dp, batch, i - npm);
   }
 }
 
-template <typename T, int D, int G>
+template <typename T, int D, int G, int GD = G>
 int launch_mixed(pf::PrefillParams pp, const dec::DecodeParams& dp, int batch, int max_e, hipStream_t stream) {
   using Geo = pf::G16<D, (int)sizeof(T)>;
   constexpr int BQ = Geo::ROWS / G;  // as in the prefill body: rows past BQ * G pad the block
@@ -73,17 +76,17 @@ int launch_mixed(pf::PrefillParams pp, const dec::DecodeParams& dp, int batch, i
   const int64_t items_dec = dec::decode_items(dp);
   const size_t lds = std::max<size_t>(Geo::LDS_BYTES, dec::decode_lds_bytes<T, D>(4));
   static std::atomic<uint64_t> lds_raised{0};  // per device, for this instantiation
-  const int lst = ensure_lds_limit(reinterpret_cast<const void*>(&mixed_attention_kernel<T, D, G>), (int)lds,
+  const int lst = ensure_lds_limit(reinterpret_cast<const void*>(&mixed_attention_kernel<T, D, G, GD>), (int)lds,
                                    lds_raised, "msgl_mixed_attention");
   if (lst != MSGL_OK) return lst;
   const int64_t groups = (items_pf + 7) / 8 + (items_dec + 7) / 8;
-  launch_main(mixed_attention_kernel<T, D, G>, dim3((unsigned)(8 * groups)), dim3(256), lds, stream, pp, dp);
+  launch_main(mixed_attention_kernel<T, D, G, GD>, dim3((unsigned)(8 * groups)), dim3(256), lds, stream, pp, dp);
   MSGL_CHECK_LAUNCH("msgl_mixed_attention");
   constexpr int HPB = 256 / (D / 4);  // heads per prefill-merge workgroup
   const int npm = pp.splits > 1 ? pp.num_tokens * ((pp.hq + HPB - 1) / HPB) : 0;
   const int ndm = dp.max_splits > 1 ? (batch * dp.hkv + 3) / 4 : 0;
   if (npm + ndm > 0) {
-    hipLaunchKernelGGL((mixed_merge_kernel<T, D, G>), dim3(npm + ndm), dim3(256), 0, stream, pp, dp, batch,
+    hipLaunchKernelGGL((mixed_merge_kernel<T, D, GD>), dim3(npm + ndm), dim3(256), 0, stream, pp, dp, batch,
                        pp.num_tokens, npm);
     MSGL_CHECK_LAUNCH("msgl_mixed_attention (merge)");
   }
@@ -101,7 +104,9 @@ int mixed_group(const pf::PrefillParams& pp, const dec::DecodeParams& dp, int ba
     case 5: return launch_mixed<T, D, 5>(pp, dp, batch, max_e, s);
     case 6: return launch_mixed<T, D, 6>(pp, dp, batch, max_e, s);
     case 7: return launch_mixed<T, D, 7>(pp, dp, batch, max_e, s);
-    case 8: return launch_mixed<T, D, 8>(pp, dp, batch, max_e, s);
+    case 8:  // the decode may run it as groups of 4 over twice the kv heads
+      return dp.hq == dp.hkv * 4 ? launch_mixed<T, D, 8, 4>(pp, dp, batch, max_e, s)
+                                 : launch_mixed<T, D, 8>(pp, dp, batch, max_e, s);
     default:
       set_error("msgl_mixed_attention: Hq/Hkv = %d not built (1-8)", group);
       return MSGL_ERR_UNSUPPORTED;

@@ -297,8 +297,6 @@ static inline DecodeWorkspace decode_workspace(int batch, int hq, int hkv, int h
 
 }  // namespace msgl
 
-int msgl::dec::decode_kv_rep(int hq, int hkv) { return head_map(hq, hkv).rep; }
-
 int64_t msgl::dec::decode_items(const DecodeParams& p) {
   // a balanced launch is chosen on the device (balanced_launch), so the grid
   // covers both forms; workgroups past the chosen one's items exit at once
