@@ -151,9 +151,10 @@ struct DecodeParams {
   int nranges;      // balanced split: key ranges of the launch (grid / ngrp)
   int64_t num_slots;
   int hq, hkv, page_size, max_splits, batch, ngrp;
-  // Query-head groups above 8 run as groups of 8 over hkv = hkv_pool * kv_rep
-  // virtual kv heads: virtual head v holds query heads [v G, v G + G) and reads
-  // pool head v / kv_rep. The pools, k_new and v_new have hkv_pool heads.
+  // Some query-head groups run over hkv = hkv_pool * kv_rep virtual kv heads
+  // (G above 8 as groups of 8; G 8 over one or two pool heads as groups of 4):
+  // virtual head v holds query heads [v G, v G + G) and reads pool head
+  // v / kv_rep. The pools, k_new, v_new and kv_scale have hkv_pool heads.
   int hkv_pool, kv_rep;
   bool planned;   // the workspace already holds this call's plan
   bool balanced;  // equal key ranges of the batch's token stream allowed (else per-request chunks)

@@ -44,6 +44,10 @@
 //    only the MFMA rows that hold query heads are processed. The reference
 //    maximum moves lazily (only when a tile's exceeds it by 2^8), so most
 //    tiles skip the accumulators' rescale.
+//  * Virtual kv heads: a group above 8 that is a multiple of 8 runs as groups
+//    of 8, and a group of 8 over one or two kv heads as groups of 4, over
+//    Hq/G' virtual kv heads that read their pool head's rows (neighbouring
+//    wavefronts, so the second read comes from L2); see head_map.
 //  * P.V on the VALU: lane (token sub-row, 16-byte d chunk) accumulates
 //    G x (16/sizeof T) fp32 outputs; P and the rescale factors go through a
 //    small per-wave LDS tile.
