@@ -40,6 +40,7 @@ Nested workloads (also runnable alone, one JSON line each):
             prefill workload's 2040 packed tokens (Qwen3-0.6B heads), 28 layers
 Other workloads (alone only):
   ceilings  a 1 GiB device copy and an 8192^3 bf16 GEMM
+  layouts   decode and ragged prefill by head layout (Hq/Hkv of the Qwen3 and Qwen2.5 families)
 """
 
 import argparse
@@ -68,7 +69,7 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--workload", default="headline",
                     choices=["headline", "decode", "decode8b", "decode_fp8", "prefill", "prefill_fp8", "mixed", "rope",
-                             "ceilings"])
+                             "ceilings", "layouts"])
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--splits", type=int, default=0, help="split-K bound (0 = library default)")
@@ -175,6 +176,7 @@ def main():
     if args.workload not in ("decode", "headline"):
         line = {"decode8b": bench_decode8b, "prefill": bench_prefill, "mixed": bench_mixed,
                 "rope": bench_rope, "decode_fp8": bench_decode_fp8, "ceilings": bench_ceilings,
+                "layouts": bench_layouts,
                 "prefill_fp8": lambda a, d: bench_prefill(a, d, fp8=True)}[args.workload](args, dev)
         print(json.dumps(line), flush=True)
         return
@@ -522,6 +524,89 @@ def _line(args, metric, value, unit, ms_per_step, workload, extra, roofline, hig
         "cpu_baseline": None,
     }
     return line
+
+
+# (Hq, Hkv) of the Qwen3 / Qwen2.5 families: decode and prefill by head layout
+DECODE_LAYOUTS = [(16, 8), (32, 8), (40, 8), (64, 8), (32, 4), (64, 4), (16, 2), (12, 2), (8, 1)]
+PREFILL_LAYOUTS = [(16, 8), (32, 8), (64, 8), (32, 4), (64, 4)]
+
+
+def bench_layouts(args, dev):
+    """Decode and ragged prefill by head layout (bf16, head_dim 128, library
+    defaults): decode over batch 64, L ~ U[1024, 3072] (seed 0), token slots;
+    prefill over the 16-request workload; 8 layer pools back to back per layout.
+    Decode throughput counts the K/V bytes each layout reads."""
+    import torch
+
+    from minisgl_hip import ops, workloads
+
+    nl = 8
+    b = 64
+    lens = np.random.default_rng(0).integers(1024, 3073, b)
+    n = int(lens.sum()) + 4096
+    c = workloads.decode_case_from_lens(lens, num_slots=n, seed=0)
+    indptr = torch.from_numpy(c.kv_indptr.astype(np.int32)).to(dev)
+    indices = torch.from_numpy(c.kv_indices.astype(np.int32)).to(dev)
+    decode = {}
+    for hq, hkv in DECODE_LAYOUTS:
+        gen = torch.Generator(device=dev).manual_seed(0)
+        kps = [torch.randn((n, hkv, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(nl)]
+        vps = [torch.randn((n, hkv, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(nl)]
+        q = torch.randn((b, hq, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        splits = args.splits or None
+
+        def run(i, q=q, kps=kps, vps=vps, splits=splits):
+            ops.paged_decode_attention(q, kps[i], vps[i], indptr, indices, D**-0.5, max_splits=splits)
+
+        sec, _ = _b2b_step_time(args, run, nl)
+        t = sec / nl
+        kv = int(lens.sum()) * hkv * D * 2 * 2
+        decode[f"{hq}/{hkv}"] = {"us_per_layer": round(t * 1e6, 2), "kv_tbs": round(kv / t / 1e12, 3)}
+        del kps, vps
+        torch.cuda.empty_cache()
+    pool = 1 << 17
+    case = workloads.prefill_case(16, 4096, 64, 512, 2048, num_slots=pool, seed=0)
+    t_tok = case.num_tokens
+    qi = torch.from_numpy(case.q_indptr).to(dev)
+    ki = torch.from_numpy(case.kv_indptr).to(dev)
+    kx = torch.from_numpy(case.kv_indices).to(dev)
+    maxe, maxs = int(case.extend_lens.max()), int(case.seq_lens.max())
+    prefill = {}
+    for hq, hkv in PREFILL_LAYOUTS:
+        flops, _ = workloads.prefill_flops_bytes(case.prefix_lens, case.extend_lens, hq, hkv, D, 2)
+        gen = torch.Generator(device=dev).manual_seed(0)
+        kps = [torch.randn((pool, hkv, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(nl)]
+        vps = [torch.randn((pool, hkv, D), generator=gen, device=dev, dtype=torch.bfloat16) for _ in range(nl)]
+        q = torch.randn((t_tok, hq, D), generator=gen, device=dev, dtype=torch.bfloat16)
+        out = torch.empty_like(q)
+        splits = ops.prefill_default_splits(16, hq, hkv, D, maxe, maxs)
+        ws = ops.prefill_workspace(16, t_tok, maxe, hq, hkv, D, splits, dev)
+
+        def run(layer, hq=hq, hkv=hkv, q=q, out=out, kps=kps, vps=vps, splits=splits, ws=ws):
+            if layer == 0:  # the work list depends only on the batch: built once per step
+                ops.prefill_plan(qi, ki, None, num_tokens=t_tok, max_extend_len=maxe, max_seq_len=maxs,
+                                 num_qo_heads=hq, num_kv_heads=hkv, head_dim=D, dtype=torch.bfloat16,
+                                 max_splits=splits, workspace=ws)
+            ops.prefill_ragged_attention(q, kps[layer], vps[layer], qi, ki, kx, None, D**-0.5, max_extend_len=maxe,
+                                         max_seq_len=maxs, max_splits=splits, out=out, workspace=ws, planned=True)
+
+        step, kern = _b2b_step_time(args, run, nl, kernel_events=True)
+        t = step / nl
+        prefill[f"{hq}/{hkv}"] = {"splits": splits, "us_per_layer": round(t * 1e6, 2),
+                                  "kernel_us": round(kern * 1e6, 2), "tflops": round(flops / t / 1e12, 1)}
+        del kps, vps
+        torch.cuda.empty_cache()
+    head = decode["16/8"]
+    return _line(
+        args, "decode and ragged-prefill µs/layer by head layout (Hq/Hkv), head_dim 128", head["us_per_layer"], "us",
+        head["us_per_layer"] * nl / 1e3,
+        "bf16, head_dim 128, library defaults, 8 layer pools back to back per layout; decode: batch 64, "
+        "L ~ U[1024, 3072] seed 0, token slots; prefill: 16 requests over cached prefixes, 2040 packed tokens",
+        {"decode": decode, "prefill": prefill},
+        {"bound": "hbm", "achieved": round(head["kv_tbs"] * 1e3, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+         "frac": round(head["kv_tbs"] * 1e3 / HBM_PEAK_GBS, 4), "traffic": None},
+        higher=False,
+    )
 
 
 def bench_decode8b(args, dev):
