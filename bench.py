@@ -555,8 +555,9 @@ def bench_layouts(args, dev):
         q = torch.randn((b, hq, D), generator=gen, device=dev, dtype=torch.bfloat16)
         splits = args.splits or None
 
-        def run(i, q=q, kps=kps, vps=vps, splits=splits):
-            ops.paged_decode_attention(q, kps[i], vps[i], indptr, indices, D**-0.5, max_splits=splits)
+        def run(i, q=q, kps=kps, vps=vps, splits=splits):  # the batch's longest request known, as in the backend
+            ops.paged_decode_attention(q, kps[i], vps[i], indptr, indices, D**-0.5, max_splits=splits,
+                                       max_seq_len=int(lens.max()))
 
         sec, _ = _b2b_step_time(args, run, nl)
         t = sec / nl

@@ -72,6 +72,12 @@ def test_abi_version_and_sizes():
     assert lib.msgl_paged_decode_default_splits(256, 8, 8192) == 6
     assert lib.msgl_paged_decode_default_splits(4096, 8, 8192) == 4
     assert lib.msgl_paged_decode_default_splits(0, 8, 8192) == 1
+    # one or two kv heads over short contexts: 16 chunks at most; long contexts keep the bound
+    assert lib.msgl_paged_decode_default_splits(64, 2, 3072) == 16
+    assert lib.msgl_paged_decode_default_splits(16, 1, 4096) == 16
+    assert lib.msgl_paged_decode_default_splits(256, 2, 3072) == 16
+    assert lib.msgl_paged_decode_default_splits(16, 1, 16384) == 64
+    assert lib.msgl_paged_decode_default_splits(64, 2, 0) > 16
 
 
 def test_prefill_sizes():
