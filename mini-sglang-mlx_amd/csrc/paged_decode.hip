@@ -603,7 +603,10 @@ int msgl::dec::decode_params(const char* fn, bool planned, const void* q, const 
     const int st = dispatch(query_op(kOpShared, 0, nullptr, &shared), dtype, kv_scale != nullptr, head_dim,
                             hm.group, fn);
     if (st != MSGL_OK) return st;
-    p.shared_head = shared;
+    // With virtual kv heads the per-head-group form keeps the virtual heads of
+    // a pool head in one workgroup, so its rows are fetched once; the
+    // shared-head form gives each its own workgroup on another XCD.
+    p.shared_head = shared && hm.rep == 1;
   }
   if (max_splits > 1) {
     const int nwaves = hm.hkv < MSGL_DECODE_WAVES_PER_WG ? hm.hkv : MSGL_DECODE_WAVES_PER_WG;
