@@ -1,11 +1,16 @@
-"""Query-head groups that are not powers of two (Hq / Hkv = 3, 5, 6, 7), which
-the reference's kernel takes as any integer ratio (attention/metal.py:122
-asserts only Hq % Hkv == 0; GQA maps q-head h to kv-head h // G,
-attention/naive.py:50-60): decode, fused store, planned decode, ragged prefill
-(one pass and key-range splits, 16-bit and fp32), fp8 pools and the single-launch
-mixed step, each against the float64 oracle or bit for bit against the calls it
-replaces. A prefill workgroup holds floor(128 / G) tokens of G heads; its
-remaining rows are padding that is computed and never stored."""
+"""Query-head groups beyond the powers of two up to 8, which the reference's
+kernel takes as any integer ratio (attention/metal.py:122 asserts only
+Hq % Hkv == 0; GQA maps q-head h to kv-head h // G, attention/naive.py:50-60):
+- Hq / Hkv = 3, 5, 6, 7 through decode, fused store, planned decode, ragged
+  prefill (one pass and key-range splits, 16-bit and fp32), fp8 pools and the
+  single-launch mixed step. A prefill workgroup holds floor(128 / G) tokens of
+  G heads; its remaining rows are padding that is computed and never stored.
+- the layouts the decode runs over virtual kv heads (groups of 16, 32 and 64
+  as groups of 8; a group of 8 over one or two kv heads as groups of 4): decode
+  in every dtype, the fused store, a stored plan and the separate merge, a
+  million keys in equal key ranges, fp8 pools.
+Each case is checked against the float64 oracle or bit for bit against the
+calls it replaces."""
 
 import numpy as np
 import pytest
